@@ -1,0 +1,236 @@
+// Band engines: the fused route + band inverse DFT (analysis, synthesis
+// adjoint) and the band DFT + gain + scatter (synthesis, analysis adjoint).
+//
+// One workgroup of 128 threads (two wave64s) owns one task: up to 2048/M
+// consecutive bands of one length M of one slice. Each band is one unit of
+// the shared FFT engine (M/16 threads, 16 values each). Tasks come from a
+// host-built table {M, first coefficient, band count, 0}; the grid is
+// tasks x batch, spread so that each XCD gets a contiguous range of
+// (task, slice) pairs and so reads each task's record rows from one L2.
+//
+// Analysis prologue (per tap j of a band, one 16-byte record):
+//   v_j = A_j Z[p1_j] + (g_j - A_j) conj Z[p2_j]
+// which is the gather of rfft(x) at the tap's bin times the window (and 1/M)
+// expressed on the packed spectrum Z: X[k] = cA(k) Z[k] + cB(k) conj Z[L-k],
+// cA = (1 - i W_N^k)/2, cB = 1 - cA; conj taps swap the roles.
+// Taps with g = 0 (outside the window support) skip both gathers.
+// Synthesis epilogue: F[pos_j] += (gr_j Re D_j, gi_j Im D_j) with fp32
+// atomics; taps with zero gains are skipped.
+// Reference semantics: radix.cu:46-114, radix_impl.cuh:27-42,100-143.
+#include "fcqt_fft.hpp"
+#include "fcqt_abi_internal.hpp"
+
+namespace fcqt {
+
+constexpr int kBandThreads = 128;
+constexpr int kBandPoints = 16 * kBandThreads;  // complex values per task
+
+constexpr int band_lds(int M) { return (kBandPoints / M) * (M + M / 16 + 1); }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int kBandLds = cmax(cmax(cmax(band_lds(32), band_lds(64)), cmax(band_lds(128), band_lds(256))),
+                              cmax(cmax(band_lds(512), band_lds(1024)), band_lds(2048)));
+
+template <int LAYOUT>
+__device__ __forceinline__ float2 load_coef(const float* __restrict__ cre, const float* __restrict__ cim, long i) {
+    if constexpr (LAYOUT == FCQT_PLANAR) return make_float2(cre[i], cim[i]);
+    else return reinterpret_cast<const float2*>(cre)[i];
+}
+
+template <int LAYOUT>
+__device__ __forceinline__ void store_coef(float* __restrict__ cre, float* __restrict__ cim, long i, float2 v) {
+    if constexpr (LAYOUT == FCQT_PLANAR) {
+        cre[i] = v.x;
+        cim[i] = v.y;
+    } else {
+        reinterpret_cast<float2*>(cre)[i] = v;
+    }
+}
+
+template <int M, int LAYOUT>
+__device__ __forceinline__ void route_band(const int4 task, const int b, const float2* __restrict__ z,
+                                           float* __restrict__ cre, float* __restrict__ cim,
+                                           const int4* __restrict__ route, const long ncoef,
+                                           const float2* __restrict__ tws, float2* lds) {
+    using P = Plan<M>;
+    const int u = threadIdx.x / P::T;
+    const int t = threadIdx.x - u * P::T;
+    const bool active = u < task.z;
+    const long cb = (long)task.y + (long)u * M;
+    const float2* zb = z + (long)b * kL;
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float2 acc = make_float2(0.0f, 0.0f);
+        if (active) {
+            const int4 rec = route[cb + t + P::T * r];
+            const float g = __int_as_float(rec.w);
+            if (g != 0.0f) {
+                const float ar = __int_as_float(rec.y);
+                const float ai = __int_as_float(rec.z);
+                const int p1 = rec.x & (kL - 1);
+                const int p2 = (int)((unsigned)rec.x >> 16) & (kL - 1);
+                const float2 z1 = zb[p1];
+                const float2 z2 = zb[p2];
+                const float br = g - ar;
+                acc.x = fmaf(ar, z1.x, fmaf(-ai, z1.y, fmaf(br, z2.x, -ai * z2.y)));
+                acc.y = fmaf(ar, z1.y, fmaf(ai, z1.x, fmaf(-ai, z2.x, -br * z2.y)));
+            }
+        }
+        v[r] = acc;
+    }
+    fft_unit<M, +1>(v, lds + u * P::US, t, tws);
+    if (active) {
+        const long ob = (long)b * ncoef + cb;
+#pragma unroll
+        for (int q = 0; q < P::QL; ++q) {
+#pragma unroll
+            for (int r = 0; r < P::RL; ++r) {
+                const int m = t + P::T * q + r * P::OS;
+                store_coef<LAYOUT>(cre, cim, ob + m, v[q * P::RL + r]);
+            }
+        }
+    }
+}
+
+template <int M, int LAYOUT>
+__device__ __forceinline__ void scatter_band(const int4 task, const int b, const float* __restrict__ cre,
+                                             const float* __restrict__ cim, float* __restrict__ f,
+                                             const int4* __restrict__ scat, const long ncoef,
+                                             const float2* __restrict__ tws, float2* lds) {
+    using P = Plan<M>;
+    const int u = threadIdx.x / P::T;
+    const int t = threadIdx.x - u * P::T;
+    const bool active = u < task.z;
+    const long cb = (long)task.y + (long)u * M;
+    const long ib = (long)b * ncoef + cb;
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        v[r] = active ? load_coef<LAYOUT>(cre, cim, ib + t + P::T * r) : make_float2(0.0f, 0.0f);
+    fft_unit<M, -1>(v, lds + u * P::US, t, tws);
+    if (active) {
+        float* fb = f + 2 * (long)b * kFStride;
+#pragma unroll
+        for (int q = 0; q < P::QL; ++q) {
+#pragma unroll
+            for (int r = 0; r < P::RL; ++r) {
+                const int m = t + P::T * q + r * P::OS;
+                const int4 rec = scat[cb + m];
+                if ((rec.y | rec.z) != 0) {
+                    const unsigned pos = min((unsigned)rec.x, (unsigned)kL);
+                    const float2 d = v[q * P::RL + r];
+                    float* p = fb + 2 * pos;
+                    unsafeAtomicAdd(p, __int_as_float(rec.y) * d.x);
+                    unsafeAtomicAdd(p + 1, __int_as_float(rec.z) * d.y);
+                }
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void decode_task(int batch, int& task, int& b) {
+    const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    task = lg / batch;
+    b = lg - task * batch;
+}
+
+template <int LAYOUT>
+__global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __restrict__ z,
+                                                              float* __restrict__ cre,
+                                                              float* __restrict__ cim,
+                                                              const int4* __restrict__ route,
+                                                              const int4* __restrict__ tasks, int batch,
+                                                              long ncoef, const float2* __restrict__ tws) {
+    __shared__ float2 lds[kBandLds];
+    int task_id, b;
+    decode_task(batch, task_id, b);
+    const int4 td = tasks[task_id];
+    switch (td.x) {
+        case 32: route_band<32, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        case 64: route_band<64, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        case 128: route_band<128, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        case 256: route_band<256, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        case 512: route_band<512, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        case 1024: route_band<1024, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        case 2048: route_band<2048, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        default: break;
+    }
+}
+
+template <int LAYOUT>
+__global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __restrict__ cre,
+                                                                const float* __restrict__ cim,
+                                                                float* __restrict__ f,
+                                                                const int4* __restrict__ scat,
+                                                                const int4* __restrict__ tasks, int batch,
+                                                                long ncoef, const float2* __restrict__ tws) {
+    __shared__ float2 lds[kBandLds];
+    int task_id, b;
+    decode_task(batch, task_id, b);
+    const int4 td = tasks[task_id];
+    switch (td.x) {
+        case 32: scatter_band<32, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        case 64: scatter_band<64, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        case 128: scatter_band<128, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        case 256: scatter_band<256, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        case 512: scatter_band<512, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        case 1024: scatter_band<1024, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        case 2048: scatter_band<2048, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        default: break;
+    }
+}
+
+static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const float* cre, const float* cim,
+                           int layout, int64_t batch) {
+    if (!tab || !rec || !cre || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
+    if (!tab->tasks || !tab->tw_stage || tab->ntasks < 1 || tab->ncoef < 1) return FCQT_EARG;
+    if ((int64_t)tab->ntasks * batch >= (int64_t)1 << 31) return FCQT_EARG;
+    if (layout != FCQT_PLANAR && layout != FCQT_INTERLEAVED) return FCQT_EARG;
+    if (layout == FCQT_PLANAR && !cim) return FCQT_EARG;
+    if (!aligned(rec, 16) || !aligned(tab->tasks, 16) || !aligned(tab->tw_stage, 16)) return FCQT_EALIGN;
+    if (layout == FCQT_PLANAR ? (!aligned(cre, 4) || !aligned(cim, 4)) : !aligned(cre, 8)) return FCQT_EALIGN;
+    return FCQT_OK;
+}
+
+}  // namespace fcqt
+
+using namespace fcqt;
+
+extern "C" int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* z,
+                                float* coef_re, float* coef_im, int layout, int64_t batch,
+                                hipStream_t stream) {
+    if (int e = check_band_args(tab, route, coef_re, coef_im, layout, batch)) return e;
+    if (!z) return FCQT_EARG;
+    if (!aligned(z, 8)) return FCQT_EALIGN;
+    const dim3 grid((unsigned)(tab->ntasks * batch));
+    const auto* zz = reinterpret_cast<const float2*>(z);
+    const auto* rr = reinterpret_cast<const int4*>(route);
+    const auto* tt = reinterpret_cast<const int4*>(tab->tasks);
+    const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
+    if (layout == FCQT_PLANAR)
+        hipLaunchKernelGGL(k_route_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, zz, coef_re,
+                           coef_im, rr, tt, (int)batch, (long)tab->ncoef, ws);
+    else
+        hipLaunchKernelGGL(k_route_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream, zz,
+                           coef_re, coef_re, rr, tt, (int)batch, (long)tab->ncoef, ws);
+    return launch_status();
+}
+
+extern "C" int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat, const float* coef_re,
+                                  const float* coef_im, int layout, float* f, int64_t batch,
+                                  hipStream_t stream) {
+    if (int e = check_band_args(tab, scat, coef_re, coef_im, layout, batch)) return e;
+    if (!f) return FCQT_EARG;
+    if (!aligned(f, 8)) return FCQT_EALIGN;
+    const dim3 grid((unsigned)(tab->ntasks * batch));
+    const auto* ss = reinterpret_cast<const int4*>(scat);
+    const auto* tt = reinterpret_cast<const int4*>(tab->tasks);
+    const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
+    if (layout == FCQT_PLANAR)
+        hipLaunchKernelGGL(k_scatter_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, coef_re,
+                           coef_im, f, ss, tt, (int)batch, (long)tab->ncoef, ws);
+    else
+        hipLaunchKernelGGL(k_scatter_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream,
+                           coef_re, coef_re, f, ss, tt, (int)batch, (long)tab->ncoef, ws);
+    return launch_status();
+}

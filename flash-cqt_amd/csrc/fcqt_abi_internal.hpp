@@ -1,0 +1,34 @@
+// Host-side helpers shared by the C-ABI launchers (argument checks and
+// launch-status capture). Not part of the public header.
+#pragma once
+
+#include <cstdint>
+#include <cstdio>
+#include <hip/hip_runtime.h>
+
+#include "../../include/flashcqt.h"
+
+namespace fcqt {
+
+// grid.x = workgroups per slice * batch must stay below 2^31; the band
+// kernel has the most workgroups per slice (< 256), so this is generous.
+constexpr int64_t kMaxBatch = 1 << 22;
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Text of the last failed launch on this host thread.
+inline char* last_error_buf() {
+    static thread_local char buf[256] = {0};
+    return buf;
+}
+
+// Status of the launch just issued: FCQT_OK, or FCQT_ELAUNCH with the HIP
+// error text recorded for fcqt_last_hip_error().
+inline int launch_status() {
+    const hipError_t e = hipGetLastError();
+    if (e == hipSuccess) return FCQT_OK;
+    std::snprintf(last_error_buf(), 256, "%s (%d)", hipGetErrorString(e), (int)e);
+    return FCQT_ELAUNCH;
+}
+
+}  // namespace fcqt

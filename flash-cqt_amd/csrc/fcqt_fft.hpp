@@ -1,0 +1,269 @@
+// Device-side FFT engine shared by every kernel of the fused CQT library.
+//
+// One "unit" is one transform of length M (a power of two, 32..2048) owned by
+// T = M/16 threads of a workgroup; every thread holds 16 complex values in
+// registers. The transform is a Stockham auto-sort decomposition
+//     M = 16 * R2 [* R3]      (R2 = 16 for M >= 256, else M/16; R3 = M/256)
+// whose first stage runs on the values each thread loaded itself (element
+// t + T*r of the unit), whose later stages exchange through LDS, and whose
+// last stage leaves element  t + T*q + r*(M/RL)  in v[q*RL + r]  (RL = last
+// radix), so the caller can store straight to global memory with unit-stride
+// lanes. Butterflies are radix 2/4/8/16 codelets on registers; only the
+// inter-stage twiddles come from a table (float64-rounded, see
+// flash_cqt/tables.py), so the transform is as accurate as fp32 allows.
+//
+// LDS layout per unit: element i at i + (i >> 4) (one pad slot every 16
+// complex values) and a unit stride of M + M/16 + 1 complex values. With
+// 8-byte accesses this keeps 16 consecutive lanes on 16 distinct bank pairs
+// for every read/write pattern below, whether consecutive lanes walk one
+// unit (band kernels, row passes) or walk across units (column pass).
+//
+// SIGN = -1 is the forward DFT  X[k] = sum x[n] e^{-2 pi i nk/M},
+// SIGN = +1 the unscaled inverse (scales are folded into the tables).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace fcqt {
+
+constexpr int kN = 65536;        // slice length (real samples)
+constexpr int kL = 32768;        // packed complex length N/2
+constexpr int kFStride = kL + 64;  // complex elements per row of the half-spectrum buffer
+
+// ------------------------------------------------------------ complex ops
+
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+
+// a * b
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+    return make_float2(fmaf(a.x, b.x, -a.y * b.y), fmaf(a.x, b.y, a.y * b.x));
+}
+// a * conj(b)
+__device__ __forceinline__ float2 cmulc(float2 a, float2 b) {
+    return make_float2(fmaf(a.x, b.x, a.y * b.y), fmaf(a.y, b.x, -a.x * b.y));
+}
+// a * (SIGN i)   i.e. a * e^{SIGN i pi/2}
+template <int SIGN>
+__device__ __forceinline__ float2 rot4(float2 a) {
+    return SIGN < 0 ? make_float2(a.y, -a.x) : make_float2(-a.y, a.x);
+}
+
+// cos / sin of e*pi/8 for e = 0..9 (the exponents a 4x4 split of a 16-point
+// DFT needs), correctly rounded double literals.
+__device__ __forceinline__ constexpr double c16(int e) {
+    return e == 0 ? 1.0 : e == 1 ? 0.92387953251128675613 : e == 2 ? 0.70710678118654752440
+         : e == 3 ? 0.38268343236508977173 : e == 4 ? 0.0 : e == 5 ? -0.38268343236508977173
+         : e == 6 ? -0.70710678118654752440 : e == 7 ? -0.92387953251128675613
+         : e == 8 ? -1.0 : -0.92387953251128675613;
+}
+__device__ __forceinline__ constexpr double s16(int e) {
+    return e == 0 ? 0.0 : e == 1 ? 0.38268343236508977173 : e == 2 ? 0.70710678118654752440
+         : e == 3 ? 0.92387953251128675613 : e == 4 ? 1.0 : e == 5 ? 0.92387953251128675613
+         : e == 6 ? 0.70710678118654752440 : e == 7 ? 0.38268343236508977173
+         : e == 8 ? 0.0 : -0.38268343236508977173;
+}
+
+// a * W16^E with W16 = e^{SIGN i pi/8}
+template <int SIGN, int E>
+__device__ __forceinline__ float2 tw16(float2 a) {
+    if constexpr (E == 0) {
+        return a;
+    } else if constexpr (E == 4) {
+        return rot4<SIGN>(a);
+    } else if constexpr (E == 2 || E == 6) {
+        // (c + SIGN i s) with |c| = |s| = 1/sqrt2
+        constexpr float h = 0.70710678118654752440f;
+        constexpr float sc = E == 2 ? 1.0f : -1.0f;  // sign of cos
+        const float re = sc * a.x - (float)SIGN * a.y;
+        const float im = sc * a.y + (float)SIGN * a.x;
+        return make_float2(re * h, im * h);
+    } else {
+        constexpr float c = (float)c16(E);
+        constexpr float s = (float)(SIGN * s16(E));
+        return make_float2(fmaf(a.x, c, -a.y * s), fmaf(a.x, s, a.y * c));
+    }
+}
+
+// -------------------------------------------------------------- codelets
+// All codelets work in place on a[0..R) and leave X[k] in a[k].
+
+template <int SIGN>
+__device__ __forceinline__ void dft2(float2* a) {
+    const float2 t = a[1];
+    a[1] = csub(a[0], t);
+    a[0] = cadd(a[0], t);
+}
+
+template <int SIGN>
+__device__ __forceinline__ void dft4v(float2& a0, float2& a1, float2& a2, float2& a3) {
+    const float2 t0 = cadd(a0, a2), t1 = csub(a0, a2);
+    const float2 t2 = cadd(a1, a3), t3 = rot4<SIGN>(csub(a1, a3));
+    a0 = cadd(t0, t2);
+    a2 = csub(t0, t2);
+    a1 = cadd(t1, t3);
+    a3 = csub(t1, t3);
+}
+
+template <int SIGN>
+__device__ __forceinline__ void dft4(float2* a) { dft4v<SIGN>(a[0], a[1], a[2], a[3]); }
+
+template <int SIGN>
+__device__ __forceinline__ void dft8(float2* a) {
+    // even / odd split: E = DFT4(a0,a2,a4,a6), O = DFT4(a1,a3,a5,a7)
+    float2 e0 = a[0], e1 = a[2], e2 = a[4], e3 = a[6];
+    float2 o0 = a[1], o1 = a[3], o2 = a[5], o3 = a[7];
+    dft4v<SIGN>(e0, e1, e2, e3);
+    dft4v<SIGN>(o0, o1, o2, o3);
+    o1 = tw16<SIGN, 2>(o1);
+    o2 = tw16<SIGN, 4>(o2);
+    o3 = tw16<SIGN, 6>(o3);
+    a[0] = cadd(e0, o0); a[4] = csub(e0, o0);
+    a[1] = cadd(e1, o1); a[5] = csub(e1, o1);
+    a[2] = cadd(e2, o2); a[6] = csub(e2, o2);
+    a[3] = cadd(e3, o3); a[7] = csub(e3, o3);
+}
+
+template <int SIGN>
+__device__ __forceinline__ void dft16(float2* a) {
+    // n = 4 n1 + n2, k = k1 + 4 k2:  X = DFT4_{n2}( W16^{n2 k1} DFT4_{n1}(a) )
+    float2 y[16];  // y[n2*4 + k1]
+#pragma unroll
+    for (int n2 = 0; n2 < 4; ++n2) {
+        float2 b0 = a[n2], b1 = a[4 + n2], b2 = a[8 + n2], b3 = a[12 + n2];
+        dft4v<SIGN>(b0, b1, b2, b3);
+        y[n2 * 4 + 0] = b0; y[n2 * 4 + 1] = b1; y[n2 * 4 + 2] = b2; y[n2 * 4 + 3] = b3;
+    }
+    y[5] = tw16<SIGN, 1>(y[5]);
+    y[6] = tw16<SIGN, 2>(y[6]);
+    y[7] = tw16<SIGN, 3>(y[7]);
+    y[9] = tw16<SIGN, 2>(y[9]);
+    y[10] = tw16<SIGN, 4>(y[10]);
+    y[11] = tw16<SIGN, 6>(y[11]);
+    y[13] = tw16<SIGN, 3>(y[13]);
+    y[14] = tw16<SIGN, 6>(y[14]);
+    y[15] = tw16<SIGN, 9>(y[15]);
+#pragma unroll
+    for (int k1 = 0; k1 < 4; ++k1) {
+        float2 b0 = y[k1], b1 = y[4 + k1], b2 = y[8 + k1], b3 = y[12 + k1];
+        dft4v<SIGN>(b0, b1, b2, b3);
+        a[k1] = b0; a[k1 + 4] = b1; a[k1 + 8] = b2; a[k1 + 12] = b3;
+    }
+}
+
+template <int R, int SIGN>
+__device__ __forceinline__ void dft(float2* a) {
+    if constexpr (R == 2) dft2<SIGN>(a);
+    else if constexpr (R == 4) dft4<SIGN>(a);
+    else if constexpr (R == 8) dft8<SIGN>(a);
+    else dft16<SIGN>(a);
+}
+
+// ------------------------------------------------------- stage twiddles
+// Table layout (complex, forward sign): for each (NS, R) in the order below,
+// entry [k][r] = W_{NS R}^{r k}, k < NS, r < R. Offsets in complex elements.
+constexpr int tw_off(int NS, int R) {
+    return NS == 16 ? (R == 2 ? 0 : R == 4 ? 32 : R == 8 ? 96 : 224)
+                    : (R == 2 ? 480 : R == 4 ? 992 : 2016);
+}
+constexpr int kTwStageLen = 4064;
+
+template <int R>
+__device__ __forceinline__ void load_tw(float2* w, const float2* __restrict__ row) {
+    const float4* p = reinterpret_cast<const float4*>(row);
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) {
+        const float4 q = p[i];
+        w[2 * i] = make_float2(q.x, q.y);
+        w[2 * i + 1] = make_float2(q.z, q.w);
+    }
+}
+
+// ------------------------------------------------------------ the plan
+
+__device__ __forceinline__ int pad16(int i) { return i + (i >> 4); }
+
+template <int M>
+struct Plan {
+    static_assert(M >= 32 && M <= 2048 && (M & (M - 1)) == 0, "band length");
+    static constexpr int T = M / 16;                     // threads per unit
+    static constexpr int R2 = M >= 256 ? 16 : M / 16;    // second radix
+    static constexpr int R3 = M > 256 ? M / 256 : 1;     // third radix (1 = none)
+    static constexpr int RL = M > 256 ? R3 : R2;         // last radix
+    static constexpr int QL = 16 / RL;                   // last-stage butterflies per thread
+    static constexpr int OS = M / RL;                    // output stride of r
+    static constexpr int US = M + M / 16 + 1;            // LDS stride per unit (complex)
+};
+
+// One Stockham stage read: butterflies j = t + T q, inputs j + r M/R,
+// twiddle W_{NS R}^{r (j mod NS)}, radix-R DFT, results into v[q R + r].
+template <int M, int R, int NS, int SIGN>
+__device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
+                                           const float2* __restrict__ tws) {
+    constexpr int T = M / 16;
+    constexpr int Q = 16 / R;
+    constexpr int STRIDE = M / R;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int j = t + T * q;
+        float2 a[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) a[r] = s[pad16(j + r * STRIDE)];
+        if constexpr (NS > 1) {
+            const int k = j & (NS - 1);
+            float2 w[R];
+            load_tw<R>(w, tws + tw_off(NS, R) + k * R);
+#pragma unroll
+            for (int r = 1; r < R; ++r) a[r] = SIGN < 0 ? cmul(a[r], w[r]) : cmulc(a[r], w[r]);
+        }
+        dft<R, SIGN>(a);
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[q * R + r] = a[r];
+    }
+}
+
+// Stockham stage write: butterfly j's result r goes to
+// (j / NS) NS R + (j mod NS) + r NS.
+template <int M, int R, int NS>
+__device__ __forceinline__ void stage_write(const float2* v, float2* s, int t) {
+    constexpr int T = M / 16;
+    constexpr int Q = 16 / R;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int j = t + T * q;
+        const int base = (j / NS) * NS * R + (j & (NS - 1));
+#pragma unroll
+        for (int r = 0; r < R; ++r) s[pad16(base + r * NS)] = v[q * R + r];
+    }
+}
+
+// Whole unit transform. Entry: v[r] = x[t + T r]; the unit's LDS region s is
+// free to write. Exit: v[q RL + r] = X[t + T q + r OS]; other threads may
+// still read s, so a caller that writes s again must barrier first.
+// Every thread of the workgroup must call this (it contains barriers).
+template <int M, int SIGN>
+__device__ __forceinline__ void fft_unit(float2* v, float2* s, int t,
+                                         const float2* __restrict__ tws) {
+    using P = Plan<M>;
+    dft16<SIGN>(v);
+    stage_write<M, 16, 1>(v, s, t);
+    __syncthreads();
+    stage_read<M, P::R2, 16, SIGN>(v, s, t, tws);
+    if constexpr (P::R3 > 1) {
+        __syncthreads();
+        stage_write<M, 16, 16>(v, s, t);
+        __syncthreads();
+        stage_read<M, P::R3, 256, SIGN>(v, s, t, tws);
+    }
+}
+
+// Spread consecutive workgroup ids over the 8 XCDs' L2s so that each XCD
+// receives a contiguous range of logical ids (the hardware dispatches ids
+// round-robin over XCDs). Bijective on [0, G).
+__device__ __forceinline__ int xcd_remap(int lin, int G) {
+    const int q = G >> 3, rem = G & 7;
+    const int xcd = lin & 7, idx = lin >> 3;
+    return xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
+}
+
+}  // namespace fcqt

@@ -1,0 +1,95 @@
+"""ctypes boundary to libflashcqt.so (the C ABI declared in include/flashcqt.h).
+
+The library is built in-tree by __graft_entry__.build() (hipcc, gfx950) into
+flash_cqt/_lib/. It is loaded after torch so that it binds to the HIP runtime
+torch already loaded (same SONAME), which makes torch's streams and hipGraph
+capture valid for its launches. There is no fallback: if the library is
+missing or does not load, every engine entry point raises.
+"""
+import ctypes
+import pathlib
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
+ABI_VERSION = 1
+PLANAR = 0
+INTERLEAVED = 1
+
+#: every symbol include/flashcqt.h declares
+EXPORTS = ("fcqt_abi_version", "fcqt_status_string", "fcqt_last_hip_error",
+           "fcqt_packed_fft_fwd", "fcqt_route_bands", "fcqt_scatter_bands",
+           "fcqt_packed_fft_inv", "fcqt_analysis", "fcqt_synthesis", "fcqt_fill_zero")
+
+
+class Tables(ctypes.Structure):
+    """Mirror of struct fcqt_tables."""
+    _fields_ = [("tw_pass", ctypes.c_void_p), ("tw_half", ctypes.c_void_p),
+                ("tw_stage", ctypes.c_void_p), ("tasks", ctypes.c_void_p),
+                ("ntasks", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("ncoef", ctypes.c_int64)]
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load():
+    """Load and type the library once; raise NativeError if unavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise NativeError(f"flash_cqt HIP library not built ({LIB_PATH}); "
+                          "run __graft_entry__.build()")
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+    except OSError as e:
+        raise NativeError(f"cannot load {LIB_PATH}: {e}") from e
+    P, I32, I64, S = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+    T = ctypes.POINTER(Tables)
+    sig = {
+        "fcqt_abi_version": ([], ctypes.c_int),
+        "fcqt_status_string": ([ctypes.c_int], ctypes.c_char_p),
+        "fcqt_last_hip_error": ([], ctypes.c_char_p),
+        "fcqt_packed_fft_fwd": ([T, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_route_bands": ([T, P, P, P, P, ctypes.c_int, I64, S], ctypes.c_int),
+        "fcqt_scatter_bands": ([T, P, P, P, ctypes.c_int, P, I64, S], ctypes.c_int),
+        "fcqt_packed_fft_inv": ([T, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_analysis": ([T, P, P, P, P, ctypes.c_int, P, P, I64, S], ctypes.c_int),
+        "fcqt_synthesis": ([T, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_fill_zero": ([P, I64, S], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    ver = lib.fcqt_abi_version()
+    if ver != ABI_VERSION:
+        raise NativeError(f"libflashcqt ABI {ver}, expected {ABI_VERSION}; rebuild")
+    _lib = lib
+    return lib
+
+
+def check(status, what):
+    if status != 0:
+        lib = load()
+        msg = lib.fcqt_status_string(status).decode()
+        hip = lib.fcqt_last_hip_error().decode()
+        raise NativeError(f"{what}: {msg}" + (f" [{hip}]" if hip else ""))
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def stream_handle():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def require_device(t, name, dtype=torch.float32):
+    if not (torch.is_tensor(t) and t.is_cuda and t.dtype == dtype and t.is_contiguous()):
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor on a GPU")

@@ -1,0 +1,193 @@
+"""FusedOctCQT: the factored CQT engine on hand-written HIP kernels (gfx950).
+
+Same surface as the reference's FusedOctCQT (fused.py:226-243, 787-801,
+918-1080): construct from an OctCQT, then
+    KR, KI = f.fwd(x)      # x [B, 65536] fp32 -> coefficient planes [B, ncoef]
+    XO     = f.bwd(KR, KI) # -> [B, 65536]
+Outputs are workspace tensors reused across calls of the same batch size (as
+in the reference); clone them to keep results. Graph capture (Graphed or
+torch.cuda.graph, i.e. hipGraph) records the launches as they are.
+
+Pipeline (all launches on the current stream, no host sync, no allocation
+after the first call for a batch size):
+  analysis   column pass -> row pass -> route + band IDFT      (3 kernels)
+  synthesis  band DFT + scatter -> column pass (retangle) -> row pass
+             (unpack, F reset)                                 (3 kernels)
+Table semantics follow fused.py:303-476; see flash_cqt/tables.py.
+"""
+import numpy as np
+import torch
+
+from . import _native
+from . import tables as T
+
+N = T.N
+HALF = N // 2
+L = T.L
+
+
+def _np_groups(cqt):
+    """numpy (idx, gv, pos, gdv, conj) per group, octave groups then side."""
+    if hasattr(cqt, "np_groups"):
+        return list(cqt.np_groups) + list(cqt.np_side_groups)
+    out = []
+    for idx, gv, pos, gdv, conj in list(cqt.groups) + list(cqt.side_groups):
+        out.append((idx.cpu().numpy(), gv.cpu().float().numpy(), pos.cpu().numpy(),
+                    gdv.cpu().float().numpy(), conj.cpu().numpy()))
+    return out
+
+
+class FusedOctCQT:
+    """Kernel tables, workspaces and launchers for one OctCQT at audio_len 65536."""
+
+    def __init__(self, cqt, device=None):
+        assert cqt.nn == N, "fused path is built for sl_len 65536"
+        dev = torch.device(device) if device is not None else torch.device(cqt.device)
+        if dev.type != "cuda":
+            raise ValueError("FusedOctCQT runs on a GPU (device 'cuda')")
+        if dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        self.dev = dev
+        self.cqt = cqt
+        self.lib = _native.load()
+
+        built = T.build(_np_groups(cqt))
+        self.gspec = built["gspec"]
+        self.ncoef = built["ncoef"]
+        self.tables = {}
+        for name in ("route", "route_b", "scat", "scat_a", "tasks", "tw_pass", "tw_half", "tw_stage"):
+            self.tables[name] = torch.as_tensor(np.ascontiguousarray(built[name])).to(dev)
+        # table bytes per direction (batch invariant, L2/MALL resident at batch)
+        self.table_bytes = {k: v.numel() * v.element_size() for k, v in self.tables.items()}
+        tb = self.tables
+        self._ct = _native.Tables(
+            tw_pass=tb["tw_pass"].data_ptr(), tw_half=tb["tw_half"].data_ptr(),
+            tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(),
+            ntasks=int(tb["tasks"].shape[0]), reserved=0, ncoef=int(self.ncoef))
+        self._ws = {}
+
+    # ------------------------------------------------------------ buffers
+
+    def _workspace(self, B):
+        """Per-batch-size buffers. F starts at zero and every synthesis call
+        leaves it at zero (the inverse row pass resets it)."""
+        if B not in self._ws:
+            with torch.cuda.device(self.dev):
+                e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)
+                z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
+                self._ws[B] = dict(Z=e(B, L, 2), W=e(B, L, 2), F=z(B, T.FSTRIDE, 2),
+                                   KR=z(B, self.ncoef), KI=z(B, self.ncoef), XO=z(B, N))
+        return self._ws[B]
+
+    def _check_x(self, x):
+        if x.dim() != 2 or x.shape[1] != N:
+            raise ValueError(f"x must be [B, {N}], got {tuple(x.shape)}")
+        _native.require_device(x, "x")
+        if x.device != self.dev:
+            raise ValueError(f"x is on {x.device}, engine on {self.dev}")
+
+    # ------------------------------------------------- raw engine launches
+    # Every launch validates its buffers first: device, contiguity, dtype and
+    # byte size must match what the kernels index, so a wrong tensor raises
+    # here instead of reaching the GPU.
+
+    def _need(self, t, nbytes, name):
+        if not torch.is_tensor(t):
+            raise ValueError(f"{name} must be a tensor")
+        if t.device != self.dev:
+            raise ValueError(f"{name} is on {t.device}, engine on {self.dev}")
+        if t.dtype not in (torch.float32, torch.complex64) or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous float32/complex64")
+        if t.numel() * t.element_size() != nbytes:
+            raise ValueError(f"{name} has {t.numel() * t.element_size()} bytes, expected {nbytes}")
+
+    def _need_coef(self, re, im, layout, B, name):
+        if layout == _native.PLANAR:
+            self._need(re, B * self.ncoef * 4, name + "_re")
+            self._need(im, B * self.ncoef * 4, name + "_im")
+        elif layout == _native.INTERLEAVED:
+            self._need(re, B * self.ncoef * 8, name)
+        else:
+            raise ValueError("layout must be PLANAR or INTERLEAVED")
+
+    def _batch(self, t, per_row_bytes, name):
+        B = t.shape[0] if t.dim() >= 1 else 0
+        if B < 1:
+            raise ValueError(f"{name} needs a leading batch dimension")
+        self._need(t, B * per_row_bytes, name)
+        return B
+
+    def packed_fft(self, x, z, work):
+        """Z = FFT_L(x[0::2] + i x[1::2]) into z [B, L, 2]."""
+        B = self._batch(x, N * 4, "x")
+        self._need(z, B * L * 8, "z")
+        self._need(work, B * L * 8, "work")
+        _native.check(self.lib.fcqt_packed_fft_fwd(self._ct, _native.ptr(x), _native.ptr(z),
+                                                   _native.ptr(work), B, _native.stream_handle()),
+                      "packed_fft_fwd")
+
+    def route_bands(self, z, out_re, out_im, layout, table="route"):
+        B = self._batch(z, L * 8, "z")
+        self._need_coef(out_re, out_im, layout, B, "out")
+        _native.check(self.lib.fcqt_route_bands(self._ct, _native.ptr(self.tables[table]), _native.ptr(z),
+                                                _native.ptr(out_re), _native.ptr(out_im), layout, B,
+                                                _native.stream_handle()), "route_bands")
+
+    def scatter_bands(self, c_re, c_im, layout, f, table="scat"):
+        B = self._batch(f, T.FSTRIDE * 8, "f")
+        self._need_coef(c_re, c_im, layout, B, "coef")
+        _native.check(self.lib.fcqt_scatter_bands(self._ct, _native.ptr(self.tables[table]), _native.ptr(c_re),
+                                                  _native.ptr(c_im), layout, _native.ptr(f), B,
+                                                  _native.stream_handle()), "scatter_bands")
+
+    def packed_ifft(self, f, y, work):
+        B = self._batch(f, T.FSTRIDE * 8, "f")
+        self._need(y, B * N * 4, "y")
+        self._need(work, B * L * 8, "work")
+        _native.check(self.lib.fcqt_packed_fft_inv(self._ct, _native.ptr(f), _native.ptr(y), _native.ptr(work),
+                                                   B, _native.stream_handle()), "packed_fft_inv")
+
+    def analysis(self, x, out_re, out_im, layout, table="route"):
+        """x [B, N] -> coefficients (planar planes or one interleaved buffer)."""
+        B = self._batch(x, N * 4, "x")
+        self._need_coef(out_re, out_im, layout, B, "out")
+        w = self._workspace(B)
+        _native.check(self.lib.fcqt_analysis(self._ct, _native.ptr(self.tables[table]), _native.ptr(x),
+                                             _native.ptr(out_re), _native.ptr(out_im), layout,
+                                             _native.ptr(w["Z"]), _native.ptr(w["W"]), B,
+                                             _native.stream_handle()), "analysis")
+
+    def synthesis(self, c_re, c_im, layout, y, table="scat"):
+        """coefficients -> y [B, N] (table 'scat' synthesis, 'scat_a' analysis adjoint)."""
+        B = self._batch(y, N * 4, "y")
+        self._need_coef(c_re, c_im, layout, B, "coef")
+        w = self._workspace(B)
+        _native.check(self.lib.fcqt_synthesis(self._ct, _native.ptr(self.tables[table]), _native.ptr(c_re),
+                                              _native.ptr(c_im), layout, _native.ptr(w["F"]),
+                                              _native.ptr(w["W"]), _native.ptr(y), B,
+                                              _native.stream_handle()), "synthesis")
+
+    # ------------------------------------------------- reference surface
+
+    def fwd(self, x):
+        """x [B, 65536] fp32 -> (KR, KI) [B, ncoef], workspace views."""
+        self._check_x(x)
+        w = self._workspace(x.shape[0])
+        self.analysis(x, w["KR"], w["KI"], _native.PLANAR)
+        return w["KR"], w["KI"]
+
+    def bwd(self, KR, KI):
+        """(KR, KI) [B, ncoef] -> XO [B, 65536], a workspace view."""
+        B = KR.shape[0]
+        if KR.shape != (B, self.ncoef) or KI.shape != (B, self.ncoef):
+            raise ValueError(f"KR, KI must be [B, {self.ncoef}]")
+        _native.require_device(KR, "KR")
+        _native.require_device(KI, "KI")
+        w = self._workspace(B)
+        self.synthesis(KR, KI, _native.PLANAR, w["XO"])
+        return w["XO"]
+
+    def blocks_view(self, KR, KI):
+        """Complex per-group blocks [B, bins, M] built from the planes."""
+        return [torch.complex(KR[:, off:off + b * M], KI[:, off:off + b * M]).view(-1, b, M)
+                for b, M, off in self.gspec]

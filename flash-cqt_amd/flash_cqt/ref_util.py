@@ -1,0 +1,61 @@
+"""Window helpers of the nonstationary Gabor bank: Hann window, window index
+ranges and the painless dual frame.
+
+The numbers must be bit-identical to the reference bank (ref_util.py:19-55),
+because the windows are the transform's definition: same float64 Hann
+recipe (scale, cos, +1, *0.5), same float32 frame diagonal accumulated band
+by band in band order. Everything is computed with numpy on the host and
+returned as numpy arrays; callers move the results to their device.
+"""
+import numpy as np
+
+
+def hann_fft_order(length):
+    """float64 Hann window of `length` with its peak at index 0 (fft order)."""
+    r = np.arange(length, dtype=np.float64)
+    r *= np.pi * 2. / length
+    r = np.cos(r)
+    r += 1.
+    r *= 0.5
+    return r
+
+
+def window_ranges(lengths, centre_bins, total):
+    """Absolute bin indices (mod nn) covered by each window, and nn.
+
+    Window i of length Lg is centred on its centre position and covers
+    [centre - Lg//2, centre + Lg - Lg//2). The centre positions are the
+    cumulative sum of the rounded centre-frequency increments, started at
+    the wrap-around increment of the last centre (ref_util.py:28-43).
+    """
+    inc = np.concatenate(((np.mod(-centre_bins[-1], total),), np.diff(centre_bins)))
+    centres = np.cumsum(inc)
+    nn = int(centres[-1])
+    centres = centres - inc[0]
+    out = []
+    for Lg, c in zip(lengths, centres):
+        lo = c - Lg // 2
+        out.append(np.mod(np.arange(lo, lo + Lg, dtype=np.int64), nn))
+    return out, nn
+
+
+def painless_dual(windows, ranges, nn, block_lengths):
+    """Canonical dual windows of a painless frame, float32.
+
+    The frame operator is diagonal: d[k] = sum_i M_i |g_i(k)|^2 over the
+    windows covering bin k (g in natural order), and the dual of window i is
+    g_i / d over its own support, back in fft order (ref_util.py:46-55).
+    Returns (duals, diagonal).
+    """
+    d = np.zeros(nn, dtype=np.float32)
+    for g, m, rng in zip(windows, block_lengths, ranges):
+        d[rng] = d[rng] + np.square(np.fft.fftshift(g)) * np.float32(m)
+    duals = [g / np.fft.ifftshift(d[rng]) for g, rng in zip(windows, ranges)]
+    return duals, d
+
+
+# names the reference exports
+def hannwin(l, device="cpu"):
+    """Reference-compatible alias: float64 torch Hann window (ref_util.py:19)."""
+    import torch
+    return torch.as_tensor(hann_fft_order(l), device=torch.device(device))

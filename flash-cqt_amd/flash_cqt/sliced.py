@@ -1,0 +1,194 @@
+"""Streamable sliced octave CQT (reference surface: sliced.py:26-209).
+
+The signal is cut into 50%-overlapped slices of sl_len samples under a Tukey
+window (flat top, Hann transitions) whose overlapped copies sum to one, each
+slice goes through the per-slice engine `self.cqt`, and the inverse
+overlap-adds the per-slice inverses. Slices are rolled by a quarter (even
+slices left, odd slices right) so the window plateau alternates, and the
+octave coefficients are rolled back by a quarter of each block.
+
+The per-slice engine is any object with fwd(x[..., sl_len]) -> (blocks, side)
+and bwd(blocks, side) -> x. engine="auto" uses the fused HIP engine
+(TrainableCQT, differentiable) on a GPU device with sl_len 65536 and the
+pure-torch OctCQT otherwise; "hip" forces the fused engine, "torch" the
+pure-torch one. Assigning self.cqt swaps engines as in the reference.
+"""
+import math
+
+import torch
+
+from .ref_util import hann_fft_order
+from .oct_cqt import OctCQT
+
+
+def makewnd(sl_len, tr_area, device="cpu", dtype=torch.float32):
+    """Tukey window of one slice, transitions centred at sl_len/4 and 3 sl_len/4."""
+    q = sl_len // 4
+    h = tr_area // 2
+    hann = torch.as_tensor(hann_fft_order(2 * tr_area), device=torch.device(device)).to(dtype)
+    w = torch.zeros(sl_len, dtype=dtype, device=torch.device(device))
+    w[q - h:q + h] = hann[tr_area:]
+    w[q + h:3 * q - h] = 1
+    w[3 * q - h:3 * q + h] = hann[:tr_area]
+    return w
+
+
+class SlicedCQT:
+    def __init__(self, num_octs=(3, 4, 2), bins_per_oct=(8, 16, 32), fs=44100,
+                 sl_len=65536, tr_area=None, device="cpu", dtype=torch.float32,
+                 engine="auto"):
+        assert sl_len % 4 == 0
+        if tr_area is None:
+            tr_area = sl_len // 4
+        assert tr_area % 2 == 0 and 0 < tr_area * 2 <= sl_len
+        self.fs = fs
+        self.sl_len = sl_len
+        self.tr_area = tr_area
+        self.H = sl_len // 4
+        self.hop = sl_len // 2
+        self.device = torch.device(device)
+        self.dtype = dtype
+
+        oct_ = OctCQT(list(num_octs), list(bins_per_oct), fs=fs, audio_len=sl_len,
+                      device=device, dtype=dtype)
+        self.oct = oct_
+        self.oct_bins = oct_.oct_bins
+        self.size_per_oct = oct_.size_per_oct
+        self.frqs_hz = oct_.frqs_hz
+        use_hip = engine == "hip" or (engine == "auto" and self.device.type == "cuda"
+                                      and sl_len == 65536)
+        if engine not in ("auto", "hip", "torch"):
+            raise ValueError("engine must be 'auto', 'hip' or 'torch'")
+        if use_hip:
+            from .trainable import TrainableCQT
+            self.cqt = TrainableCQT(oct_, device)
+        else:
+            self.cqt = oct_
+        self.tw = makewnd(sl_len, tr_area, device=device, dtype=dtype)
+        self._roll = [m // 4 for m in self.size_per_oct]
+
+    # ------------------------------------------------------------ latency
+
+    def latency_ms(self, sl_len=None):
+        """Algorithmic latency of the scheme: one full slice."""
+        return 1000.0 * (sl_len if sl_len is not None else self.sl_len) / self.fs
+
+    def lowest_fmin(self, sl_len=None):
+        """Lowest fmin whose analysis window still fits a slice (sl_len >= 8 fs q / f)."""
+        sl = sl_len if sl_len is not None else self.sl_len
+        n0 = 1
+        while n0 < len(self.oct_bins) and self.oct_bins[n0] == self.oct_bins[0]:
+            n0 += 1
+        b0 = self.oct_bins[0]
+        step = 2.0 ** ((n0 + 1) / ((n0 + 1) * b0 - 1))
+        q0 = math.sqrt(step) / (step - 1.0) / 2.0
+        return 8.0 * self.fs * q0 / sl
+
+    def latency_table(self, sl_lens=(8192, 16384, 32768, 65536, 131072)):
+        need = float(self.frqs_hz[0])
+        lines = [f"{'sl_len':>8} {'latency_ms':>11} {'lowest_fmin_hz':>15}   covers fmin {need:.1f} hz"]
+        for sl in sl_lens:
+            fmin = self.lowest_fmin(sl)
+            lines.append(f"{sl:>8} {self.latency_ms(sl):>11.1f} {fmin:>15.1f}   "
+                         f"{'yes' if fmin <= need else 'no'}")
+        return "\n".join(lines)
+
+    # ------------------------------------------------------------ slicing
+
+    def _num_slices(self, L):
+        quarters = -(-L // self.H)
+        return (quarters + 1) // 2 + 1
+
+    def _slice(self, x):
+        """[B, C, L] -> windowed, rolled slices [B, C, S, sl_len]."""
+        B, C, L = x.shape
+        H = self.H
+        S = self._num_slices(L)
+        quarters = -(-L // H)
+        xp = torch.cat([x.new_zeros(B, C, 2 * H), x,
+                        x.new_zeros(B, C, quarters * H - L + 3 * H)], dim=-1)
+        sl = xp.unfold(-1, 4 * H, 2 * H)[:, :, :S, :] * self.tw
+        even = (torch.arange(S, device=x.device) % 2 == 0).view(1, 1, -1, 1)
+        return torch.where(even, torch.roll(sl, -H, -1), torch.roll(sl, H, -1))
+
+    def _arrange(self, blocks, S, fwd):
+        """Undo (fwd) / redo (bwd) the quarter roll on the octave blocks;
+        side blocks stay rolled."""
+        out = []
+        sgn = 1 if fwd else -1
+        for c, r in zip(blocks, self._roll):
+            even = (torch.arange(S, device=c.device) % 2 == 0).view(1, 1, -1, 1, 1)
+            out.append(torch.where(even, torch.roll(c, sgn * r, -1), torch.roll(c, -sgn * r, -1)))
+        return out
+
+    # --------------------------------------------------- whole buffer api
+
+    def fwd(self, x):
+        """x [B, C, L] -> (blocks, side): blocks[i] [B, C, oct_bins[i], S*size_per_oct[i]]
+        in time order along the last axis, side (dc, nyq) per slice [B, C, S, 1, M]."""
+        B, C, _ = x.shape
+        sl = self._slice(x)
+        S = sl.shape[2]
+        blocks, side = self.cqt.fwd(sl)
+        blocks = self._arrange(blocks, S, fwd=True)
+        blocks = [c.permute(0, 1, 3, 2, 4).reshape(B, C, b, S * m)
+                  for c, b, m in zip(blocks, self.oct_bins, self.size_per_oct)]
+        return blocks, side
+
+    def bwd(self, blocks, side=None, length=None):
+        """Inverse of fwd; length trims the tail padding."""
+        B, C = blocks[0].shape[:2]
+        S = blocks[0].shape[-1] // self.size_per_oct[0]
+        blocks = [c.reshape(B, C, b, S, m).permute(0, 1, 3, 2, 4)
+                  for c, b, m in zip(blocks, self.oct_bins, self.size_per_oct)]
+        blocks = self._arrange(blocks, S, fwd=False)
+        y = self.cqt.bwd(blocks, side)
+        H = self.H
+        even = (torch.arange(S, device=y.device) % 2 == 0).view(1, 1, -1, 1)
+        y = torch.where(even, torch.roll(y, H, -1), torch.roll(y, -H, -1))
+        out = y.new_zeros(B, C, (S + 1) * 2 * H)
+        out[..., :S * 2 * H] += y[..., :2 * H].reshape(B, C, -1)
+        out[..., 2 * H:] += y[..., 2 * H:].reshape(B, C, -1)
+        out = out[..., 2 * H:]
+        return out[..., :length] if length is not None else out
+
+    # --------------------------------------------- streaming, bounded state
+
+    def stream_fwd(self, chunks):
+        """chunks yields [B, C, hop] pieces (pad the last one); yields one
+        (blocks, side) per slice, blocks[i] [B, C, oct_bins[i], M_i].
+        State: one half slice of input."""
+        prev = None
+        k = 0
+
+        def one(prev, chunk, k):
+            sl = torch.cat([prev, chunk], dim=-1) * self.tw
+            sl = torch.roll(sl, -self.H if k % 2 == 0 else self.H, -1)
+            blocks, side = self.cqt.fwd(sl.unsqueeze(2))
+            # a single slice is "even" for _arrange; odd slices roll the other way
+            blocks = self._arrange(blocks, 1, fwd=(k % 2 == 0))
+            return [c[:, :, 0] for c in blocks], [c[:, :, 0] for c in side]
+
+        for chunk in chunks:
+            if prev is None:
+                prev = torch.zeros_like(chunk)
+            yield one(prev, chunk, k)
+            prev = chunk
+            k += 1
+        yield one(prev, torch.zeros_like(prev), k)
+
+    def stream_bwd(self, slice_coeffs):
+        """slice_coeffs yields (blocks, side) as stream_fwd emits; yields
+        [B, C, hop] output pieces one slice behind. State: one half slice."""
+        tail = None
+        k = 0
+        for blocks, side in slice_coeffs:
+            blocks = [c.unsqueeze(2) for c in blocks]
+            side = [c.unsqueeze(2) for c in side] if side is not None else None
+            blocks = self._arrange(blocks, 1, fwd=(k % 2 != 0))
+            y = self.cqt.bwd(blocks, side)[:, :, 0]
+            y = torch.roll(y, self.H if k % 2 == 0 else -self.H, -1)
+            if tail is not None:
+                yield tail + y[..., :self.hop]
+            tail = y[..., self.hop:]
+            k += 1

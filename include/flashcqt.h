@@ -1,0 +1,140 @@
+/* flashcqt.h -- C ABI of the MI355X (gfx950) fused factored CQT engine.
+ *
+ * The library (libflashcqt.so, built with hipcc) implements the hot path of
+ * the factored constant-Q transform for 65536-sample slices:
+ *   analysis   x -> packed half-length FFT -> route + band inverse DFTs -> C
+ *   synthesis  C -> band DFTs + gain + scatter -> packed inverse FFT -> y
+ * and both adjoints by running the same kernels with different tables.
+ *
+ * Conventions
+ *   - Every buffer is device memory allocated by the caller; the library
+ *     never allocates or frees. Tables are built on the host (the Python
+ *     package flash_cqt/tables.py) and uploaded by the caller.
+ *   - Complex buffers are interleaved fp32 pairs (re, im), 8-byte aligned.
+ *     Record tables (int32 quadruples) must be 16-byte aligned.
+ *   - All work is enqueued asynchronously on `stream` (any HIP stream,
+ *     including one under hipGraph capture); no call synchronises, allocates
+ *     or issues hipMemset, so every call can be captured into a graph.
+ *   - Return value: FCQT_OK (0), or an FCQT_E* code. Argument errors are
+ *     detected before any HIP call is made.
+ *   - Calls that share a workspace must be ordered on one stream.
+ *
+ * Fixed geometry (the reference's fused path hard-requires it,
+ * fused.py:230): N = 65536 real samples per slice, L = N/2 = 32768.
+ */
+#ifndef FLASHCQT_H
+#define FLASHCQT_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FCQT_ABI_VERSION 1
+
+#define FCQT_N 65536          /* real samples per slice */
+#define FCQT_L 32768          /* packed complex length */
+#define FCQT_FSTRIDE 32832    /* complex elements per batch row of the half-spectrum buffer F (>= L+1) */
+#define FCQT_TW_STAGE_LEN 4064 /* complex elements of the stage twiddle table */
+#define FCQT_TW_PASS_LEN 32768 /* complex elements of the pass twiddle table [128][256] */
+#define FCQT_TW_HALF_LEN 32768 /* complex elements of the retangle twiddle table W_65536^i */
+
+/* status codes */
+#define FCQT_OK 0
+#define FCQT_EARG 1      /* null pointer, bad size or bad enum */
+#define FCQT_EALIGN 2    /* pointer misaligned for its element type */
+#define FCQT_ELAUNCH 3   /* kernel launch failed (HIP error) */
+
+/* coefficient layouts */
+#define FCQT_PLANAR 0       /* re and im in two [batch][ncoef] fp32 planes */
+#define FCQT_INTERLEAVED 1  /* one [batch][ncoef] complex buffer, pass it as re, im ignored */
+
+/* Host-side descriptor of the uploaded, batch-invariant tables. */
+typedef struct fcqt_tables {
+    const float*   tw_pass;   /* [128][256] complex, W_32768^(k1*n2) at k1*256+n2 */
+    const float*   tw_half;   /* [32768] complex, W_65536^i */
+    const float*   tw_stage;  /* [FCQT_TW_STAGE_LEN] complex band/pass stage twiddles */
+    const int32_t* tasks;     /* [ntasks][4] band tasks: M, coefficient offset, band count, 0 */
+    int32_t        ntasks;
+    int32_t        reserved;
+    int64_t        ncoef;     /* complex coefficients per slice (132992 for [3,4,2]/[8,16,32]) */
+} fcqt_tables;
+
+/* ABI version of the loaded library (FCQT_ABI_VERSION). */
+int fcqt_abi_version(void);
+
+/* Static text for a status code. */
+const char* fcqt_status_string(int status);
+
+/* Text of the last HIP error seen by a launcher on this thread ("" if none). */
+const char* fcqt_last_hip_error(void);
+
+/* Packed forward FFT of real slices.
+ *   x    [batch][65536] fp32 (8-byte aligned)
+ *   z    [batch][32768] complex, out: Z = FFT_32768(x[0::2] + i x[1::2]), natural order
+ *   work [batch][32768] complex scratch
+ * Replaces the even/odd pack copies (trainable.py:81-82) and fft3
+ * (packedfft.cu:100-126); two launches (column pass, row pass). */
+int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* z, float* work,
+                        int64_t batch, hipStream_t stream);
+
+/* Route + band inverse DFTs: every coefficient c of band b is
+ *   C_b[m] = sum_j (A_j Z[p1_j] + (g_j - A_j) conj Z[p2_j]) e^{+2 pi i jm/M_b}
+ * with one 16-byte record {p1 | p2<<16, Re A, Im A, g} per tap (the 1/M and
+ * every window/untangle constant folded in). With the analysis table this is
+ * the analysis; with the dual-window table it is the synthesis adjoint.
+ *   z      [batch][32768] complex (from fcqt_packed_fft_fwd)
+ *   coef   layout FCQT_PLANAR: coef_re, coef_im [batch][ncoef] fp32
+ *          layout FCQT_INTERLEAVED: coef_re is [batch][ncoef] complex, coef_im unused
+ *   route  [ncoef][4] int32 records
+ * Replaces fwd_bands (radix.cu:46-62). */
+int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* z,
+                     float* coef_re, float* coef_im, int layout,
+                     int64_t batch, hipStream_t stream);
+
+/* Band DFTs + per-tap gain + scatter-add into the half spectrum F:
+ *   D_b = DFT_{M_b}(C_b);  F[pos_j] += (gr_j Re D_b[j], gi_j Im D_b[j])
+ * with one 16-byte record {pos, gr, gi, 0} per tap; gr = gi = 0 skips a tap.
+ * With the synthesis table this is the synthesis front half; with the
+ * analysis-adjoint table it is the analysis adjoint front half.
+ *   f  [batch][FCQT_FSTRIDE] complex accumulator; MUST be zero on entry
+ *      (fcqt_fill_zero once; fcqt_packed_fft_inv re-zeroes it).
+ * Uses fp32 atomics: the summation order of overlapping taps (at most 3 per
+ * bin) is not fixed, so results may differ in the last bits between runs.
+ * Replaces inv_bands (radix.cu:64-91) and adj_bands (radix.cu:93-114). */
+int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat,
+                       const float* coef_re, const float* coef_im, int layout,
+                       float* f, int64_t batch, hipStream_t stream);
+
+/* Packed inverse real FFT: y = irfft_65536(F[0..32768]) (imaginary parts of
+ * bins 0 and 32768 ignored, as irfft does), then F is reset to zero.
+ *   f    [batch][FCQT_FSTRIDE] complex, in; zero on return
+ *   y    [batch][65536] fp32 out (8-byte aligned)
+ *   work [batch][32768] complex scratch
+ * Replaces inv_tail (packedfft.cu:233-254) and the F memsets
+ * (trainable.py:104-105). */
+int fcqt_packed_fft_inv(const fcqt_tables* tab, float* f, float* y, float* work,
+                        int64_t batch, hipStream_t stream);
+
+/* Analysis in one call: fcqt_packed_fft_fwd then fcqt_route_bands.
+ * z and work are [batch][32768] complex scratch. */
+int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
+                  float* coef_re, float* coef_im, int layout,
+                  float* z, float* work, int64_t batch, hipStream_t stream);
+
+/* Synthesis in one call: fcqt_scatter_bands then fcqt_packed_fft_inv.
+ * f must be zero on entry and is zero on return. */
+int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat,
+                   const float* coef_re, const float* coef_im, int layout,
+                   float* f, float* work, float* y, int64_t batch, hipStream_t stream);
+
+/* Zero n floats with a fill kernel (graph-capture safe, no hipMemsetAsync). */
+int fcqt_fill_zero(float* buf, int64_t n, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHCQT_H */

@@ -1,0 +1,281 @@
+"""numpy simulator of the HIP kernels' schedules (test infrastructure).
+
+Replays, thread by thread (vectorised over threads), the exact index
+arithmetic of flash-cqt_amd/csrc: the Stockham stages of fcqt_fft.hpp with
+the padded LDS layout, the column / row passes of packed_fft.hip and the
+band prologue / epilogue of bands.hip, using the product's own tables
+(flash_cqt/tables.py). Butterfly codelets are exact DFTs here; every LDS and
+global index is asserted in bounds. This is the CPU gate that runs before
+any GPU time, like the reference's schedule reference
+(bench/radix_reference.py) and table gates (bench/radix_gpu.py:51-120).
+"""
+import numpy as np
+
+from flash_cqt import tables as T
+
+L = T.L
+N = T.N
+
+
+def pad16(i):
+    return i + (i >> 4)
+
+
+class Plan:
+    def __init__(self, M):
+        self.M = M
+        self.T = M // 16
+        self.R2 = 16 if M >= 256 else M // 16
+        self.R3 = M // 256 if M > 256 else 1
+        self.RL = self.R3 if M > 256 else self.R2
+        self.QL = 16 // self.RL
+        self.OS = M // self.RL
+        self.US = M + M // 16 + 1
+
+
+def _dft(a, R, sign):
+    """DFT of length R over the last axis; sign -1 forward, +1 unscaled inverse."""
+    return np.fft.fft(a, axis=-1) if sign < 0 else np.fft.ifft(a, axis=-1) * R
+
+
+_TWS = None
+
+
+def tws():
+    global _TWS
+    if _TWS is None:
+        t = T.stage_twiddles()
+        _TWS = t[:, 0].astype(np.complex128) + 1j * t[:, 1].astype(np.complex128)
+    return _TWS
+
+
+def tw_off(ns, r):
+    off = 0
+    for a, b in T.STAGE_ORDER:
+        if (a, b) == (ns, r):
+            return off
+        off += a * b
+    raise KeyError((ns, r))
+
+
+def stage_write(v, s, t, M, R, NS, base):
+    """v [U, T, 16] -> LDS s (flat) at base[u] + pad16(pos)."""
+    P = Plan(M)
+    Q = 16 // R
+    for q in range(Q):
+        j = t + P.T * q
+        b = (j // NS) * NS * R + (j & (NS - 1))
+        for r in range(R):
+            idx = pad16(b + r * NS)
+            assert idx.max() < P.US - 1 + 1 and idx.min() >= 0
+            s[base[:, None] + idx[None, :]] = v[:, :, q * R + r]
+
+
+def stage_read(s, t, M, R, NS, sign, base):
+    P = Plan(M)
+    Q = 16 // R
+    stride = M // R
+    out = np.empty((base.size, P.T, 16), dtype=np.complex128)
+    for q in range(Q):
+        j = t + P.T * q
+        a = np.empty((base.size, P.T, R), dtype=np.complex128)
+        for r in range(R):
+            idx = pad16(j + r * stride)
+            assert idx.max() < P.US and idx.min() >= 0
+            a[:, :, r] = s[base[:, None] + idx[None, :]]
+        if NS > 1:
+            k = j & (NS - 1)
+            off = tw_off(NS, R)
+            rows = off + k[:, None] * R + np.arange(R)[None, :]
+            assert rows.max() < T.TW_STAGE_LEN
+            w = tws()[rows]
+            if sign > 0:
+                w = np.conj(w)
+            a = a * w[None, :, :]
+        out[:, :, q * R:(q + 1) * R] = _dft(a, R, sign)
+    return out
+
+
+def fft_unit(v, M, sign):
+    """v [U, T, 16] with v[u, t, r] = x_u[t + T r] -> v[u, t, q RL + r] = X_u[t + T q + r OS]."""
+    P = Plan(M)
+    U = v.shape[0]
+    t = np.arange(P.T)
+    s = np.full(U * P.US, np.nan + 0j)
+    base = np.arange(U) * P.US
+    v = _dft(v, 16, sign)
+    stage_write(v, s, t, M, 16, 1, base)
+    v = stage_read(s, t, M, P.R2, 16, sign, base)
+    if P.R3 > 1:
+        stage_write(v, s, t, M, 16, 16, base)
+        v = stage_read(s, t, M, P.R3, 256, sign, base)
+    return v
+
+
+def unit_output_index(M):
+    """[T, 16] natural output index held by (thread, register slot)."""
+    P = Plan(M)
+    t = np.arange(P.T)[:, None]
+    out = np.empty((P.T, 16), dtype=np.int64)
+    for q in range(P.QL):
+        for r in range(P.RL):
+            out[:, q * P.RL + r] = t[:, 0] + P.T * q + r * P.OS
+    return out
+
+
+# ------------------------------------------------------------ packed FFT
+
+def packed_fft_fwd(x):
+    """Column + row pass of packed_fft.hip on x [B, N] -> Z [B, L] natural."""
+    x = np.asarray(x, dtype=np.float64)
+    B = x.shape[0]
+    z = x[:, 0::2] + 1j * x[:, 1::2]
+    twp = T.pass_twiddles()
+    twp = twp[:, 0] + 1j * twp[:, 1]
+    Y = np.empty((B, L), dtype=np.complex128)
+    c = np.arange(16)
+    tt = np.arange(8)
+    for b in range(B):
+        for cg in range(16):
+            n2 = cg * 16 + c                                  # [16]
+            v = np.empty((16, 8, 16), dtype=np.complex128)    # [unit=c, t, r]
+            for r in range(16):
+                idx = 256 * (tt[None, :] + 8 * r) + n2[:, None]
+                assert idx.max() < L
+                v[:, :, r] = z[b][idx]
+            v = fft_unit(v, 128, -1)
+            for q in range(2):
+                for r in range(8):
+                    k1 = tt + 8 * q + 16 * r
+                    o = k1[None, :] * 256 + n2[:, None]
+                    assert o.max() < L
+                    Y[b][o] = v[:, :, q * 8 + r] * twp[o]
+    return _row_pass(Y, inverse=False)
+
+
+def _row_pass(Y, inverse):
+    B = Y.shape[0]
+    out = np.empty((B, L), dtype=np.complex128)
+    t = np.arange(16)
+    for b in range(B):
+        for rg in range(8):
+            k1 = rg * 16 + np.arange(16)
+            v = np.empty((16, 16, 16), dtype=np.complex128)
+            for r in range(16):
+                v[:, :, r] = Y[b][(k1[:, None] * 256) + (t[None, :] + 16 * r)]
+            v = fft_unit(v, 256, -1)
+            # transpose through LDS then store at k1 + 128 k2
+            for u in range(16):
+                k2 = np.arange(16) + 16 * u      # kg = 0..15
+                o = k1[:, None] + 128 * k2[None, :]
+                assert o.max() < L
+                out[b][o] = v[:, k2 % 16, k2 // 16]
+    if inverse:
+        return out / L
+    return out
+
+
+def packed_fft_inv(F):
+    """Retangle column pass + row pass: F [B, L+1] -> y [B, N]."""
+    F = np.asarray(F, dtype=np.complex128)
+    B = F.shape[0]
+    twn = T.half_twiddles()
+    twn = twn[:, 0] + 1j * twn[:, 1]
+    twp = T.pass_twiddles()
+    twp = twp[:, 0] + 1j * twp[:, 1]
+    Y = np.empty((B, L), dtype=np.complex128)
+    c = np.arange(16)
+    tt = np.arange(8)
+    for b in range(B):
+        for cg in range(16):
+            n2 = cg * 16 + c
+            v = np.empty((16, 8, 16), dtype=np.complex128)
+            for r in range(16):
+                i = 256 * (tt[None, :] + 8 * r) + n2[:, None]
+                f0 = F[b][i].copy()
+                f1 = F[b][L - i].copy()
+                zero = i == 0
+                f0[zero] = f0[zero].real
+                f1[zero] = f1[zero].real
+                e = 0.5 * (f0 + np.conj(f1))
+                d = 0.5 * (f0 - np.conj(f1))
+                o = d * np.conj(twn[i])
+                v[:, :, r] = np.conj(e + 1j * o)
+            v = fft_unit(v, 128, -1)
+            for q in range(2):
+                for r in range(8):
+                    k1 = tt + 8 * q + 16 * r
+                    o = k1[None, :] * 256 + n2[:, None]
+                    Y[b][o] = v[:, :, q * 8 + r] * twp[o]
+    zp = _row_pass(Y, inverse=True)
+    y = np.empty((B, N))
+    y[:, 0::2] = zp.real
+    y[:, 1::2] = -zp.imag
+    return y
+
+
+# ----------------------------------------------------------- band engines
+
+def _decode(rec):
+    f = rec.view(np.float32)
+    return rec[:, 0], f[:, 1].astype(np.float64), f[:, 2].astype(np.float64), f[:, 3].astype(np.float64)
+
+
+def route_bands(Z, route, tasks, ncoef):
+    """bands.hip route_band on Z [B, L] -> coefficients [B, ncoef]."""
+    B = Z.shape[0]
+    out = np.full((B, ncoef), np.nan + 0j)
+    pp, ar, ai, g = _decode(route)
+    p1 = pp & (L - 1)
+    p2 = (pp.astype(np.int64) >> 16) & (L - 1)
+    A = ar + 1j * ai
+    Bc = (g - ar) - 1j * ai
+    for M, first, nb, _ in tasks.tolist():
+        P = Plan(M)
+        U = T.POINTS_PER_TASK // M
+        assert nb <= U
+        t = np.arange(P.T)
+        for b in range(B):
+            v = np.zeros((U, P.T, 16), dtype=np.complex128)
+            for u in range(nb):
+                cb = first + u * M
+                for r in range(16):
+                    j = cb + t + P.T * r
+                    assert j.max() < ncoef
+                    live = g[j] != 0
+                    val = A[j] * Z[b][p1[j]] + Bc[j] * np.conj(Z[b][p2[j]])
+                    v[u, :, r] = np.where(live, val, 0)
+            v = fft_unit(v, M, +1)
+            oi = unit_output_index(M)
+            for u in range(nb):
+                cb = first + u * M
+                assert cb + oi.max() < ncoef
+                out[b][cb + oi] = v[u]
+    return out
+
+
+def scatter_bands(C, scat, tasks, ncoef):
+    """bands.hip scatter_band: C [B, ncoef] -> F [B, L+1] accumulated."""
+    B = C.shape[0]
+    F = np.zeros((B, L + 1), dtype=np.complex128)
+    pos, gr, gi, _ = _decode(scat)
+    for M, first, nb, _ in tasks.tolist():
+        P = Plan(M)
+        U = T.POINTS_PER_TASK // M
+        t = np.arange(P.T)
+        oi = unit_output_index(M)
+        for b in range(B):
+            v = np.zeros((U, P.T, 16), dtype=np.complex128)
+            for u in range(nb):
+                cb = first + u * M
+                for r in range(16):
+                    v[u, :, r] = C[b][cb + t + P.T * r]
+            v = fft_unit(v, M, -1)
+            for u in range(nb):
+                cb = first + u * M
+                j = (cb + oi).reshape(-1)
+                d = v[u].reshape(-1)
+                live = (gr[j] != 0) | (gi[j] != 0)
+                p = np.minimum(pos[j], L)
+                np.add.at(F[b], p[live], gr[j][live] * d[live].real + 1j * gi[j][live] * d[live].imag)
+    return F

@@ -1,0 +1,82 @@
+"""C-ABI checks that need no GPU: the library loads, exports exactly what
+include/flashcqt.h declares, and rejects bad arguments before any HIP call."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "flashcqt.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(fcqt_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from flash_cqt import _native
+    return _native.load()
+
+
+def test_header_and_python_agree():
+    from flash_cqt import _native
+    assert declared() == sorted(_native.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.fcqt_abi_version() == 1
+
+
+def test_status_strings(lib):
+    assert lib.fcqt_status_string(0) == b"ok"
+    assert b"argument" in lib.fcqt_status_string(1)
+
+
+def test_argument_errors_detected_before_any_launch(lib):
+    from flash_cqt._native import Tables
+    tab = Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=1, reserved=0, ncoef=1)
+    bad = Tables(tw_pass=0, tw_half=0, tw_stage=0, tasks=0, ntasks=0, reserved=0, ncoef=0)
+    s = ctypes.c_void_p(0)
+    p = ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(4100)
+    null = ctypes.c_void_p(0)
+    EARG, EALIGN = 1, 2
+    # null table descriptor / buffers / batch 0
+    assert lib.fcqt_packed_fft_fwd(None, p, p, p, 1, s) == EARG
+    assert lib.fcqt_packed_fft_fwd(ctypes.byref(tab), null, p, p, 1, s) == EARG
+    assert lib.fcqt_packed_fft_fwd(ctypes.byref(tab), p, p, p, 0, s) == EARG
+    assert lib.fcqt_packed_fft_fwd(ctypes.byref(bad), p, p, p, 1, s) == EARG
+    # misaligned complex buffer
+    assert lib.fcqt_packed_fft_fwd(ctypes.byref(tab), odd, p, p, 1, s) == EALIGN
+    # bad layout, null im plane for planar
+    assert lib.fcqt_route_bands(ctypes.byref(tab), p, p, p, p, 7, 1, s) == EARG
+    assert lib.fcqt_route_bands(ctypes.byref(tab), p, p, p, null, 0, 1, s) == EARG
+    assert lib.fcqt_route_bands(ctypes.byref(tab), odd, p, p, p, 0, 1, s) == EALIGN
+    assert lib.fcqt_scatter_bands(ctypes.byref(tab), p, p, p, 0, null, 1, s) == EARG
+    assert lib.fcqt_packed_fft_inv(ctypes.byref(tab), p, p, p, -3, s) == EARG
+    assert lib.fcqt_analysis(ctypes.byref(tab), null, p, p, p, 0, p, p, 1, s) == EARG
+    assert lib.fcqt_synthesis(ctypes.byref(tab), p, p, p, 0, odd, p, p, 1, s) == EALIGN
+    assert lib.fcqt_fill_zero(null, 10, s) == EARG
+    assert lib.fcqt_fill_zero(p, 0, s) == 0  # nothing to do, no launch
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from flash_cqt import _native
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "nope.so")
+    with pytest.raises(_native.NativeError):
+        _native.load()
+
+
+def test_engine_refuses_cpu_device(pkg_cqt_cpu):
+    from flash_cqt.fused import FusedOctCQT
+    with pytest.raises(ValueError):
+        FusedOctCQT(pkg_cqt_cpu, "cpu")

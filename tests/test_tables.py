@@ -1,0 +1,100 @@
+"""CPU gates of the product's transform definition and factored tables.
+
+The package's OctCQT tables must equal the reference tables bit for bit
+(golden hashes); its pure-torch fwd/bwd must agree with the oracle; and the
+factored tables, replayed through the kernels' exact schedule
+(tests/kernel_sim.py), must reproduce the oracle's analysis, synthesis and
+both adjoints (the analogue of the reference's CPU table gates,
+bench/radix_gpu.py:51-120 and bench/autograd_check.py)."""
+import numpy as np
+import torch
+
+import kernel_sim as ks
+from golden.golden_inputs import inputs
+from oracle.cqt_oracle import snr_db
+from test_oracle import group_hashes
+
+N = 65536
+
+
+def test_package_tables_bit_exact(pkg_cqt_cpu, golden):
+    c = pkg_cqt_cpu
+    assert group_hashes(c.np_groups + c.np_side_groups) == golden["group_table_sha256"].tolist()
+    assert np.array_equal(c.bank.M.numpy(), golden["bank_M"])
+    torch_groups = [tuple(t.numpy() for t in g) for g in c.groups + c.side_groups]
+    assert group_hashes(torch_groups) == golden["group_table_sha256"].tolist()
+
+
+def test_package_torch_transform_matches_oracle(pkg_cqt_cpu, oracle):
+    x, _ = inputs()
+    with torch.no_grad():
+        bl, sd = pkg_cqt_cpu.fwd(torch.from_numpy(x))
+        y = pkg_cqt_cpu.bwd(bl, sd)
+    obl, osd = oracle.fwd(x)
+    got = torch.cat([c.reshape(2, -1) for c in list(bl) + list(sd)], -1).numpy()
+    assert snr_db(oracle.flatten(obl, osd), got) > 125
+    assert snr_db(oracle.bwd(obl, osd), y.numpy()) > 125
+
+
+def test_task_table_covers_every_coefficient_once(factored_tables):
+    t = factored_tables
+    seen = np.zeros(t["ncoef"], dtype=np.int64)
+    for M, first, nb, _ in t["tasks"].tolist():
+        seen[first:first + nb * M] += 1
+    assert (seen == 1).all()
+
+
+def test_record_fields(factored_tables, pkg_cqt_cpu):
+    """Route records: p1/p2 are the packed-spectrum taps of the gather bin,
+    g is the window / M, and B = g - A reproduces cB g (cA + cB = 1)."""
+    t = factored_tables
+    groups = pkg_cqt_cpu.np_groups + pkg_cqt_cpu.np_side_groups
+    k = np.concatenate([g[0].reshape(-1) for g in groups])
+    cf = np.concatenate([g[4].reshape(-1) for g in groups])
+    M = np.concatenate([np.full(g[0].size, g[0].shape[1]) for g in groups])
+    gv = np.concatenate([g[1].reshape(-1) for g in groups]).astype(np.float64)
+    r = t["route"]
+    p1 = r[:, 0] & 0xFFFF
+    p2 = (r[:, 0] >> 16) & 0xFFFF
+    L = N // 2
+    assert np.array_equal(np.where(cf, (L - k) % L, k % L), p1)
+    assert np.array_equal(np.where(cf, k % L, (L - k) % L), p2)
+    g = r[:, 3].view(np.float32).astype(np.float64)
+    assert np.array_equal(g * M, gv.astype(np.float32).astype(np.float64))
+
+
+def test_schedule_sim_analysis_and_synthesis(factored_tables, oracle):
+    t = factored_tables
+    x, _ = inputs()
+    x = x[:1].astype(np.float64)
+    Z = ks.packed_fft_fwd(x)
+    assert snr_db(np.fft.fft(x[:, 0::2] + 1j * x[:, 1::2]), Z) > 140
+    C = ks.route_bands(Z, t["route"], t["tasks"], t["ncoef"])
+    obl, osd = oracle.fwd(x)
+    Cref = oracle.flatten(obl, osd)
+    assert snr_db(Cref, C) > 140
+    F = ks.scatter_bands(Cref, t["scat"], t["tasks"], t["ncoef"])
+    y = ks.packed_fft_inv(F)
+    assert snr_db(oracle.bwd(obl, osd), y) > 140
+
+
+def test_schedule_sim_adjoints(factored_tables, oracle):
+    t = factored_tables
+    rs = np.random.RandomState(12)
+    G = rs.standard_normal((1, t["ncoef"])) + 1j * rs.standard_normal((1, t["ncoef"]))
+    F = ks.scatter_bands(G, t["scat_a"], t["tasks"], t["ncoef"])
+    gx = ks.packed_fft_inv(F)
+    assert snr_db(oracle.fwd_adjoint(*oracle.unflatten(G)), gx) > 140
+    u = rs.standard_normal((1, N))
+    Zu = ks.packed_fft_fwd(u)
+    gC = ks.route_bands(Zu, t["route_b"], t["tasks"], t["ncoef"])
+    assert snr_db(oracle.flatten(*oracle.bwd_adjoint(u)), gC) > 140
+
+
+def test_inverse_tail_drops_edge_imaginary_parts():
+    """irfft semantics: Im F[0] and Im F[L] do not reach the output."""
+    rs = np.random.RandomState(2)
+    L = N // 2
+    F = rs.standard_normal((1, L + 1)) + 1j * rs.standard_normal((1, L + 1))
+    y = ks.packed_fft_inv(F)
+    assert snr_db(np.fft.irfft(F, n=N), y) > 140
