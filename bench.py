@@ -1,0 +1,354 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused factored CQT round trip on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one fused round trip (analysis + synthesis) of a batch of
+65536-sample fp32 slices, replayed from a hipGraph with the input already in
+device memory. The timed region is exactly K replays of the batch-64 graph
+(BASELINE configs[2]); batch 1 (configs[1], sinusoids + noise) and batch 16
+are measured the same way (median of event-timed replays) and reported in
+"per_batch". Beside them, in the same run:
+  - the hipFFT-call baseline: the package's pure-torch OctCQT (torch.fft ->
+    hipFFT/rocFFT) on the GPU, graph-captured, same inputs;
+  - the host-core baseline: the oracle's torch port of the reference
+    OctCQT on the box's CPU cores, a bounded sample (cpu_baseline).
+Per-kernel launch durations are timed with hipEvents on the launch stream
+(graphs of back-to-back launches); "roofline" reports the dominant kernel's
+algorithmic bytes per launch over its duration against 8 TB/s.
+
+Extra modes (for rocprofv3 counter runs): --kernels-only runs a few
+launches of every kernel plus a plain copy of known size (the calibration
+kernel for FETCH_SIZE / WRITE_SIZE) and prints nothing else.
+"""
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "flash-cqt_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+N = 65536
+L = N // 2
+FS = 44100
+METRIC = "CQT round trips/sec (fwd+inv, 65536 samples) at batch 1/16/64; HBM GB/s"
+PEAK_GBPS = 8000.0
+# algorithmic bytes per slice (fp32; tables excluded, batch invariant)
+SLICE_RT_BYTES = 2 * 262144 + 2 * 1063936     # x in, coefficients out, coefficients in, y out
+KERNEL_BYTES = {
+    "packed_fft": 262144 + 262144,            # x in, Z out
+    "route_bands": 262144 + 1063936,          # Z in, coefficients out
+    "scatter_bands": 1063936 + 262152,        # coefficients in, half spectrum out
+    "packed_ifft": 262152 + 262144,           # half spectrum in, y out
+}
+KERNEL_LAUNCHES = {"packed_fft": 2, "route_bands": 1, "scatter_bands": 1, "packed_ifft": 2}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def sinusoids(seed=0):
+    """8 unit sinusoids, log-uniform 43 Hz..20 kHz, random phase, + N(0, 0.01^2)."""
+    rs = np.random.RandomState(seed)
+    f = np.exp(rs.uniform(np.log(43.0), np.log(20000.0), 8))
+    ph = rs.uniform(0, 2 * np.pi, 8)
+    n = np.arange(N)
+    x = np.sum(np.sin(2 * np.pi * f[:, None] * n[None, :] / FS + ph[:, None]), 0)
+    return (x + 0.01 * rs.standard_normal(N))[None, :].astype(np.float32)
+
+
+def randn(B, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(B, N, generator=g, dtype=torch.float32)
+
+
+def snr_db(ref, got):
+    ref = ref.double()
+    e = ref.square().sum()
+    d = (ref - got.double()).square().sum()
+    return float("inf") if float(d) == 0 else float(10 * torch.log10(e / d))
+
+
+def capture(fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    return g, out
+
+
+def median_ms(fn, reps=50, warm=3):
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        ts.append(s.elapsed_time(e))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def replay_matches_eager(g, out, eager, poison, reps=3):
+    """Poison what the graph must write, replay, compare with eager; repeat
+    with eager work in between."""
+    worst = float("inf")
+    for r in range(reps):
+        for t in poison:
+            t.fill_(1e9 if r % 2 == 0 else float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        worst = min(worst, snr_db(eager, out))
+        _ = torch.randn(4096, device=out.device).sum().item()
+    return worst
+
+
+# ----------------------------------------------------------- baselines
+
+def torch_fft_baseline(cqt_gpu, x):
+    """Graph-captured pure-torch OctCQT round trip (hipFFT); eager if the
+    replay does not reproduce eager results."""
+    fn = lambda: cqt_gpu.bwd(*cqt_gpu.fwd(x))
+    with torch.no_grad():
+        eager = fn().clone()
+        try:
+            g, out = capture(fn)
+            ok = replay_matches_eager(g, out, eager, [out]) > 100
+        except Exception as e:  # capture unsupported by a library call
+            log(f"hipFFT baseline capture failed: {e}")
+            ok = False
+        if ok:
+            return median_ms(g.replay), "hipGraph", eager
+        return median_ms(fn), "eager", eager
+
+
+def cpu_baseline(budget_s=12.0, max_reps=400):
+    """The reference OctCQT algorithm (oracle torch port) on the host cores,
+    batch 1, configs[1] input; bounded to about budget_s of CPU work."""
+    from oracle.torch_port import TorchPortOctCQT
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    port = TorchPortOctCQT()
+    x = torch.from_numpy(sinusoids())
+    with torch.no_grad():
+        y = port.bwd(*port.fwd(x))
+        ts = []
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end and len(ts) < max_reps:
+            t0 = time.perf_counter()
+            port.bwd(*port.fwd(x))
+            ts.append(time.perf_counter() - t0)
+    ts.sort()
+    med = ts[len(ts) // 2]
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": 1.0 / med, "unit": "slice round trips/s", "cores": cores, "kind": "port",
+            "sample": f"{len(ts)} batch-1 round trips of the configs[1] input (median "
+                      f"{med * 1e3:.2f} ms), oracle/torch_port.py, torch CPU {cores} threads, {model}",
+            "snr_db": snr_db(x, y)}
+
+
+# ---------------------------------------------------------- kernel timings
+
+def kernel_timings(f, B, reps):
+    """Average duration per launch of each engine call at batch B (graphs of
+    `reps` back-to-back launches, hipEvents on the launch stream)."""
+    from flash_cqt import _native
+    dev = f.dev
+    w = f._workspace(B)
+    x = randn(B, 1).to(dev)
+    kr = torch.empty(B, f.ncoef, device=dev)
+    ki = torch.empty(B, f.ncoef, device=dev)
+    y = torch.empty(B, N, device=dev)
+    f.packed_fft(x, w["Z"], w["W"])
+    f.route_bands(w["Z"], kr, ki, _native.PLANAR)
+    calls = {
+        "packed_fft": lambda: f.packed_fft(x, w["Z"], w["W"]),
+        "route_bands": lambda: f.route_bands(w["Z"], kr, ki, _native.PLANAR),
+        "scatter_bands": lambda: f.scatter_bands(kr, ki, _native.PLANAR, w["F"]),
+        "packed_ifft": lambda: f.packed_ifft(w["F"], y, w["W"]),
+    }
+    out = {}
+    for name, fn in calls.items():
+        def many(fn=fn):
+            for _ in range(reps):
+                fn()
+        g, _ = capture(many)
+        ms = median_ms(g.replay, reps=10, warm=2) / reps
+        per = ms / KERNEL_LAUNCHES[name]
+        alg = KERNEL_BYTES[name] * B
+        out[name] = {"ms_per_call": ms, "launches": KERNEL_LAUNCHES[name],
+                     "ms_per_launch": per, "alg_bytes_per_call": alg,
+                     "gbps": alg / (ms * 1e-3) / 1e9}
+    torch.cuda.synchronize()
+    return out
+
+
+def kernels_only(f, B, reps):
+    """A few launches of each kernel and one plain copy of known size, for
+    rocprofv3 --pmc runs (FETCH_SIZE / WRITE_SIZE calibration)."""
+    from flash_cqt import _native
+    dev = f.dev
+    w = f._workspace(B)
+    x = randn(B, 1).to(dev)
+    kr = torch.empty(B, f.ncoef, device=dev)
+    ki = torch.empty(B, f.ncoef, device=dev)
+    y = torch.empty(B, N, device=dev)
+    src = torch.ones(16 * 1024 * 1024, device=dev)      # 64 MiB
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        f.packed_fft(x, w["Z"], w["W"])
+        f.route_bands(w["Z"], kr, ki, _native.PLANAR)
+        f.scatter_bands(kr, ki, _native.PLANAR, w["F"])
+        f.packed_ifft(w["F"], y, w["W"])
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"kernels-only: B={B} reps={reps}; copy kernel moves 64 MiB read + 64 MiB write per launch")
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-lib-baseline", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the engine is single-GPU (batch sharding across "
+              "GPUs needs no communication and is not exercised here); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    from flash_cqt import OctCQT
+    from flash_cqt.fused import FusedOctCQT
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cqt_gpu = OctCQT([3, 4, 2], [8, 16, 32], fs=FS, audio_len=N, device=dev)
+    f = FusedOctCQT(cqt_gpu, dev)
+    if args.kernels_only:
+        kernels_only(f, args.batch, max(1, args.kernel_reps // 4))
+        return
+
+    batches = sorted({1, 16, 64, args.batch})
+    per_batch = {}
+    graphs = {}
+    for B in batches:
+        x = (torch.from_numpy(sinusoids()) if B == 1 else randn(B, 0)).to(dev)
+        w = f._workspace(B)
+        fn = lambda x=x: f.bwd(*f.fwd(x))
+        with torch.no_grad():
+            eager = fn().clone()
+            g, out = capture(fn)
+            rep_db = replay_matches_eager(g, out, eager, [w["KR"], w["KI"], w["Z"], w["W"], w["XO"]])
+            rt_rows = min(snr_db(x[b], eager[b]) for b in range(B))
+            KR, KI = f.fwd(x)
+            ours = torch.complex(KR, KI).clone()
+            tb, ts = cqt_gpu.fwd(x)
+            ref = torch.cat([c.reshape(B, -1) for c in list(tb) + list(ts)], -1)
+            coef_db = snr_db(torch.view_as_real(ref), torch.view_as_real(ours))
+        graphs[B] = (g, x)
+        ms = median_ms(g.replay)
+        per_batch[B] = {"ms": ms, "round_trips_per_s": B / (ms * 1e-3),
+                        "hbm_gbps": B * SLICE_RT_BYTES / (ms * 1e-3) / 1e9,
+                        "roundtrip_snr_db_min_row": rt_rows, "coef_snr_db_vs_torch_fft": coef_db,
+                        "replay_vs_eager_db": rep_db,
+                        "input": "configs[1] sinusoids+noise" if B == 1 else "randn N(0,1) seed 0"}
+        if not args.no_lib_baseline:
+            bms, mode, bout = torch_fft_baseline(cqt_gpu, x)
+            per_batch[B].update({"hipfft_baseline_ms": bms, "hipfft_baseline_mode": mode,
+                                 "speedup_vs_hipfft": bms / ms,
+                                 "hipfft_baseline_roundtrip_snr_db": snr_db(x, bout)})
+        log(f"B={B}: {ms:.4f} ms  {per_batch[B]['round_trips_per_s']:.0f} rt/s  "
+            f"{per_batch[B]['hbm_gbps']:.0f} GB/s  rt {rt_rows:.1f} dB  coef {coef_db:.1f} dB"
+            + (f"  hipFFT {per_batch[B]['hipfft_baseline_ms']:.4f} ms ({mode})" if not args.no_lib_baseline else ""))
+
+    # ---- the timed region: exactly K replays of the batch graph
+    B = args.batch
+    g, _ = graphs[B]
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    value = B / (ms_step * 1e-3)
+    gbps = B * SLICE_RT_BYTES / (ms_step * 1e-3) / 1e9
+
+    kern = kernel_timings(f, B, args.kernel_reps)
+    single = {k: v for k, v in kern.items() if v["launches"] == 1}
+    dom = max(single, key=lambda k: single[k]["ms_per_launch"])
+    ach = kern[dom]["gbps"]
+    roof = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": PEAK_GBPS, "unit": "GB/s",
+            "frac": ach / PEAK_GBPS, "traffic": None,
+            "alg_bytes_per_launch": kern[dom]["alg_bytes_per_call"],
+            "ms_per_launch": kern[dom]["ms_per_launch"], "batch": B}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+
+    line = {
+        "metric": METRIC, "value": value, "unit": "slice round trips/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"fused fp32 CQT round trip (analysis+synthesis), batch {B} "
+                               f"(configs[2]; batch 1 = configs[1] in per_batch), hipGraph replay",
+                   "batch": B, "slice_len": N,
+                   "layout": "OctCQT([3,4,2],[8,16,32],fs=44100), 154 bands, 132992 coefficients",
+                   "parallelism": "single GPU"},
+        "hbm_gbps": gbps, "hbm_frac": gbps / PEAK_GBPS, "wall_s_timed": wall,
+        "per_batch": {str(k): v for k, v in per_batch.items()},
+        "kernels": kern,
+        "table_bytes": f.table_bytes,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -56,14 +56,14 @@ extern "C" int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const
     return fcqt_route_bands(tab, route, z, coef_re, coef_im, layout, batch, stream);
 }
 
-extern "C" int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const float* coef_re,
-                              const float* coef_im, int layout, float* f, float* work, float* y,
-                              int64_t batch, hipStream_t stream) {
-    if (!scat || !f || !work || !y) return FCQT_EARG;
+extern "C" int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* ovf,
+                              const float* coef_re, const float* coef_im, int layout, float* f,
+                              float* work, float* y, int64_t batch, hipStream_t stream) {
+    if (!scat || !ovf || !f || !work || !y) return FCQT_EARG;
     // validate the second half before launching the first, so an argument
     // error never leaves F half-written
     if (!tab || !tab->tw_pass || !tab->tw_half || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
-    if (!aligned(f, 16) || !aligned(y, 8) || !aligned(work, 8)) return FCQT_EALIGN;
+    if (!aligned(f, 16) || !aligned(y, 8) || !aligned(work, 8) || !aligned(ovf, 4)) return FCQT_EALIGN;
     if (int e = fcqt_scatter_bands(tab, scat, coef_re, coef_im, layout, f, batch, stream)) return e;
-    return fcqt_packed_fft_inv(tab, f, y, work, batch, stream);
+    return fcqt_packed_fft_inv(tab, ovf, f, y, work, batch, stream);
 }

@@ -14,8 +14,12 @@
 // expressed on the packed spectrum Z: X[k] = cA(k) Z[k] + cB(k) conj Z[L-k],
 // cA = (1 - i W_N^k)/2, cB = 1 - cA; conj taps swap the roles.
 // Taps with g = 0 (outside the window support) skip both gathers.
-// Synthesis epilogue: F[pos_j] += (gr_j Re D_j, gi_j Im D_j) with fp32
-// atomics; taps with zero gains are skipped.
+// Synthesis epilogue: tap j stores (gr_j Re D_j, gi_j Im D_j) to its own
+// slot of the half-spectrum buffer F (the record holds the slot target:
+// plane P0 or P1 at the tap's bin, or an overflow slot for bins with more
+// than two taps); taps with zero gains are skipped. No atomics: each slot has
+// exactly one writer, so the result is bitwise reproducible, and the
+// inverse column pass sums a bin's slots on load.
 // Reference semantics: radix.cu:46-114, radix_impl.cuh:27-42,100-143.
 #include "fcqt_fft.hpp"
 #include "fcqt_abi_internal.hpp"
@@ -109,7 +113,7 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
         v[r] = active ? load_coef<LAYOUT>(cre, cim, ib + t + P::T * r) : make_float2(0.0f, 0.0f);
     fft_unit<M, -1>(v, lds + u * P::US, t, tws);
     if (active) {
-        float* fb = f + 2 * (long)b * kFStride;
+        float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
 #pragma unroll
         for (int q = 0; q < P::QL; ++q) {
 #pragma unroll
@@ -117,11 +121,9 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
                 const int m = t + P::T * q + r * P::OS;
                 const int4 rec = scat[cb + m];
                 if ((rec.y | rec.z) != 0) {
-                    const unsigned pos = min((unsigned)rec.x, (unsigned)kL);
+                    const unsigned slot = min((unsigned)rec.x, (unsigned)(kFRow - 1));
                     const float2 d = v[q * P::RL + r];
-                    float* p = fb + 2 * pos;
-                    unsafeAtomicAdd(p, __int_as_float(rec.y) * d.x);
-                    unsafeAtomicAdd(p + 1, __int_as_float(rec.z) * d.y);
+                    fb[slot] = make_float2(__int_as_float(rec.y) * d.x, __int_as_float(rec.z) * d.y);
                 }
             }
         }
@@ -221,7 +223,7 @@ extern "C" int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat, c
                                   hipStream_t stream) {
     if (int e = check_band_args(tab, scat, coef_re, coef_im, layout, batch)) return e;
     if (!f) return FCQT_EARG;
-    if (!aligned(f, 8)) return FCQT_EALIGN;
+    if (!aligned(f, 16)) return FCQT_EALIGN;
     const dim3 grid((unsigned)(tab->ntasks * batch));
     const auto* ss = reinterpret_cast<const int4*>(scat);
     const auto* tt = reinterpret_cast<const int4*>(tab->tasks);

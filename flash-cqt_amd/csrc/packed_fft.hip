@@ -10,12 +10,13 @@
 //                per workgroup = 128-byte runs).
 // Forward: the column pass reads the real slice as complex pairs
 // z[n] = x[2n] + i x[2n+1] directly (the pack costs nothing).
-// Inverse: the column pass retangles the half spectrum on load,
+// Inverse: the column pass sums each bin's scatter slots (two dense planes
+// plus, for the few bins flagged in the table's overflow bitmask, two
+// overflow slots) and retangles the half spectrum on load,
 //   E = (F[i] + conj F[L-i])/2,  O = (F[i] - conj F[L-i])/2 * conj(W_N^i),
 //   W = conj(E + i O),
 // the row pass runs the same forward FFT and unpacks on store,
-//   y[2k] = Re/L, y[2k+1] = -Im/L,
-// then resets its share of F to zero for the next scatter.
+//   y[2k] = Re/L, y[2k+1] = -Im/L.
 // Reference semantics: packedfft.cu:100-169 (three radix-32 passes, separate
 // retangle/unpack launches and a permuted output order there).
 #include "fcqt_fft.hpp"
@@ -30,11 +31,26 @@ constexpr int kRowWgs = 128 / kRowsPerWg;      // 8 workgroups per slice
 
 // ------------------------------------------------------------ column pass
 
+// Value of half-spectrum bin i (0 <= i <= L) from its scatter slots.
+__device__ __forceinline__ float2 load_bin(const float2* __restrict__ fb, const int* __restrict__ ovf, int i) {
+    float2 v = cadd(fb[i], fb[kFStride + i]);
+    const unsigned w = (unsigned)ovf[i >> 5];
+    const unsigned bit = 1u << (i & 31);
+    if (w & bit) {
+        int k = ovf[kMaskWords + (i >> 5)] + __popc(w & (bit - 1u));
+        k = min(k, kOvfCap - 1);
+        const float2* o = fb + 2 * kFStride + 2 * k;
+        v = cadd(v, cadd(o[0], o[1]));
+    }
+    return v;
+}
+
 template <bool INVERSE>
 __global__ __launch_bounds__(128) void k_col_pass(const float2* __restrict__ in,
                                                   float2* __restrict__ out,
                                                   const float2* __restrict__ twp,
                                                   const float2* __restrict__ twn,
+                                                  const int* __restrict__ ovf,
                                                   const float2* __restrict__ tws) {
     using P = Plan<128>;
     __shared__ float2 lds[kColsPerWg * P::US];
@@ -49,12 +65,12 @@ __global__ __launch_bounds__(128) void k_col_pass(const float2* __restrict__ in,
 #pragma unroll
         for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
     } else {
-        const float2* fb = in + (long)b * kFStride;
+        const float2* fb = in + (long)b * kFRow;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int i = 256 * (t + 8 * r) + n2;
-            float2 f0 = fb[i];
-            float2 f1 = fb[kL - i];
+            float2 f0 = load_bin(fb, ovf, i);
+            float2 f1 = load_bin(fb, ovf, kL - i);
             if (i == 0) {  // bins 0 and L are real for irfft
                 f0.y = 0.0f;
                 f1.y = 0.0f;
@@ -84,7 +100,6 @@ __global__ __launch_bounds__(128) void k_col_pass(const float2* __restrict__ in,
 template <bool INVERSE>
 __global__ __launch_bounds__(256) void k_row_pass(const float2* __restrict__ in,
                                                   float2* __restrict__ out,
-                                                  float2* __restrict__ fzero,
                                                   const float2* __restrict__ tws) {
     using P = Plan<256>;
     __shared__ float2 lds[kRowsPerWg * P::US];
@@ -125,13 +140,6 @@ __global__ __launch_bounds__(256) void k_row_pass(const float2* __restrict__ in,
             const float2 w = s2[pad16(k2)];
             yo[kk1 + 128 * k2] = make_float2(w.x * sc, -w.y * sc);
         }
-        // reset this workgroup's share of F: complex [rg*4096, (rg+1)*4096),
-        // and the Nyquist bin L in the last workgroup
-        float4* fb = reinterpret_cast<float4*>(fzero + (long)b * kFStride + rg * 4096);
-        const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) fb[threadIdx.x + 256 * u] = zero4;
-        if (rg == kRowWgs - 1 && threadIdx.x == 0) fzero[(long)b * kFStride + kL] = make_float2(0.f, 0.f);
     }
 }
 
@@ -149,29 +157,27 @@ extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
     hipLaunchKernelGGL(k_col_pass<false>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
                        reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
-                       reinterpret_cast<const float2*>(tab->tw_pass), nullptr, tws);
+                       reinterpret_cast<const float2*>(tab->tw_pass), nullptr, nullptr, tws);
     if (int e = launch_status()) return e;
     hipLaunchKernelGGL(k_row_pass<false>, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
-                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(z),
-                       nullptr, tws);
+                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(z), tws);
     return launch_status();
 }
 
-extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, float* f, float* y, float* work,
-                                   int64_t batch, hipStream_t stream) {
-    if (!tab || !f || !y || !work || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
+extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float* f, float* y,
+                                   float* work, int64_t batch, hipStream_t stream) {
+    if (!tab || !ovf || !f || !y || !work || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
     if (!tab->tw_pass || !tab->tw_half || !tab->tw_stage) return FCQT_EARG;
     if (!aligned(f, 16) || !aligned(y, 8) || !aligned(work, 8) || !aligned(tab->tw_pass, 8) ||
-        !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
+        !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16) || !aligned(ovf, 4))
         return FCQT_EALIGN;
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
     hipLaunchKernelGGL(k_col_pass<true>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
                        reinterpret_cast<const float2*>(f), reinterpret_cast<float2*>(work),
                        reinterpret_cast<const float2*>(tab->tw_pass),
-                       reinterpret_cast<const float2*>(tab->tw_half), tws);
+                       reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const int*>(ovf), tws);
     if (int e = launch_status()) return e;
     hipLaunchKernelGGL(k_row_pass<true>, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
-                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(y),
-                       reinterpret_cast<float2*>(f), tws);
+                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(y), tws);
     return launch_status();
 }

@@ -58,9 +58,9 @@ def load():
         "fcqt_packed_fft_fwd": ([T, P, P, P, I64, S], ctypes.c_int),
         "fcqt_route_bands": ([T, P, P, P, P, ctypes.c_int, I64, S], ctypes.c_int),
         "fcqt_scatter_bands": ([T, P, P, P, ctypes.c_int, P, I64, S], ctypes.c_int),
-        "fcqt_packed_fft_inv": ([T, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_packed_fft_inv": ([T, P, P, P, P, I64, S], ctypes.c_int),
         "fcqt_analysis": ([T, P, P, P, P, ctypes.c_int, P, P, I64, S], ctypes.c_int),
-        "fcqt_synthesis": ([T, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_synthesis": ([T, P, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
         "fcqt_fill_zero": ([P, I64, S], ctypes.c_int),
     }
     for name, (args, res) in sig.items():

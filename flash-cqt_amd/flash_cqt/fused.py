@@ -11,8 +11,9 @@ torch.cuda.graph, i.e. hipGraph) records the launches as they are.
 Pipeline (all launches on the current stream, no host sync, no allocation
 after the first call for a batch size):
   analysis   column pass -> row pass -> route + band IDFT      (3 kernels)
-  synthesis  band DFT + scatter -> column pass (retangle) -> row pass
-             (unpack, F reset)                                 (3 kernels)
+  synthesis  band DFT + slot scatter -> column pass (slot sum, retangle)
+             -> row pass (unpack)                              (3 kernels)
+No kernel uses atomics: every result is bitwise reproducible.
 Table semantics follow fused.py:303-476; see flash_cqt/tables.py.
 """
 import numpy as np
@@ -55,7 +56,8 @@ class FusedOctCQT:
         self.gspec = built["gspec"]
         self.ncoef = built["ncoef"]
         self.tables = {}
-        for name in ("route", "route_b", "scat", "scat_a", "tasks", "tw_pass", "tw_half", "tw_stage"):
+        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks",
+                     "tw_pass", "tw_half", "tw_stage"):
             self.tables[name] = torch.as_tensor(np.ascontiguousarray(built[name])).to(dev)
         # table bytes per direction (batch invariant, L2/MALL resident at batch)
         self.table_bytes = {k: v.numel() * v.element_size() for k, v in self.tables.items()}
@@ -69,15 +71,18 @@ class FusedOctCQT:
     # ------------------------------------------------------------ buffers
 
     def _workspace(self, B):
-        """Per-batch-size buffers. F starts at zero and every synthesis call
-        leaves it at zero (the inverse row pass resets it)."""
+        """Per-batch-size buffers. Each scatter table gets its own half-spectrum
+        slot buffer (F for synthesis, FA for the analysis adjoint), zeroed once:
+        the slots a table never writes must stay zero."""
         if B not in self._ws:
             with torch.cuda.device(self.dev):
                 e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)
                 z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
-                self._ws[B] = dict(Z=e(B, L, 2), W=e(B, L, 2), F=z(B, T.FSTRIDE, 2),
+                self._ws[B] = dict(Z=e(B, L, 2), W=e(B, L, 2), F=z(B, T.FROW, 2), FA=z(B, T.FROW, 2),
                                    KR=z(B, self.ncoef), KI=z(B, self.ncoef), XO=z(B, N))
         return self._ws[B]
+
+    _FBUF = {"scat": "F", "scat_a": "FA"}
 
     def _check_x(self, x):
         if x.dim() != 2 or x.shape[1] != N:
@@ -134,17 +139,19 @@ class FusedOctCQT:
                                                 _native.stream_handle()), "route_bands")
 
     def scatter_bands(self, c_re, c_im, layout, f, table="scat"):
-        B = self._batch(f, T.FSTRIDE * 8, "f")
+        B = self._batch(f, T.FROW * 8, "f")
         self._need_coef(c_re, c_im, layout, B, "coef")
         _native.check(self.lib.fcqt_scatter_bands(self._ct, _native.ptr(self.tables[table]), _native.ptr(c_re),
                                                   _native.ptr(c_im), layout, _native.ptr(f), B,
                                                   _native.stream_handle()), "scatter_bands")
 
-    def packed_ifft(self, f, y, work):
-        B = self._batch(f, T.FSTRIDE * 8, "f")
+    def packed_ifft(self, f, y, work, table="scat"):
+        """y = irfft of the half spectrum held in f's slots (filled with `table`)."""
+        B = self._batch(f, T.FROW * 8, "f")
         self._need(y, B * N * 4, "y")
         self._need(work, B * L * 8, "work")
-        _native.check(self.lib.fcqt_packed_fft_inv(self._ct, _native.ptr(f), _native.ptr(y), _native.ptr(work),
+        _native.check(self.lib.fcqt_packed_fft_inv(self._ct, _native.ptr(self.tables["ovf_" + table]),
+                                                   _native.ptr(f), _native.ptr(y), _native.ptr(work),
                                                    B, _native.stream_handle()), "packed_fft_inv")
 
     def analysis(self, x, out_re, out_im, layout, table="route"):
@@ -162,8 +169,9 @@ class FusedOctCQT:
         B = self._batch(y, N * 4, "y")
         self._need_coef(c_re, c_im, layout, B, "coef")
         w = self._workspace(B)
-        _native.check(self.lib.fcqt_synthesis(self._ct, _native.ptr(self.tables[table]), _native.ptr(c_re),
-                                              _native.ptr(c_im), layout, _native.ptr(w["F"]),
+        _native.check(self.lib.fcqt_synthesis(self._ct, _native.ptr(self.tables[table]),
+                                              _native.ptr(self.tables["ovf_" + table]), _native.ptr(c_re),
+                                              _native.ptr(c_im), layout, _native.ptr(w[self._FBUF[table]]),
                                               _native.ptr(w["W"]), _native.ptr(y), B,
                                               _native.stream_handle()), "synthesis")
 

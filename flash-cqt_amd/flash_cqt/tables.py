@@ -13,11 +13,22 @@ Everything the kernels need that does not depend on the batch:
            (2/N)(1 - [k in {0, L}]/2) (the transpose of irfft is (2/N) rfft
            with bins 0 and L halved; the band's transpose of the forward DFT
            is the unscaled inverse DFT).
-  scat     synthesis record per tap {pos, gdv, gdv, 0}: F[pos] += gdv DFT(C).
-  scat_a   analysis-adjoint record {idx, gr, gi, 0} with
+  scat     synthesis record per tap {slot target of pos, gdv, gdv, 0}:
+           the half spectrum is F[pos] = sum over taps of gdv DFT(C).
+  scat_a   analysis-adjoint record {slot target of idx, gr, gi, 0} with
            gr = g (N/2)/M (1 + edge), gi = -+gr (1 - edge): the transpose of
            rfft is (N/2) irfft with bins 0 and L doubled, of a conj tap the
            conjugate, of the band's 1/M inverse DFT the forward DFT / M.
+           Scatter without atomics: the live taps of one bin (at most 4) are
+           ranked; rank 0 and 1 own dense planes P0[bin], P1[bin], ranks 2-3
+           own two slots of a compact overflow area indexed by the bin's
+           position among the bins of degree > 2. Every (slot, bin) has one
+           writer, the set of written slots is fixed by the table, and slots
+           never written stay zero, so F needs zeroing only once.
+  ovf_*    per scatter table, int32 [2 * MASK_WORDS]: bit b of word w marks
+           bin 32 w + b as having overflow slots; the second half holds the
+           number of overflow bins before word w (the overflow index of a
+           bin is that prefix plus the popcount of the lower bits).
   tasks    band tasks {M, first coefficient, band count, 0}: consecutive
            bands of one group, at most POINTS / M per task.
   tw_pass  W_L^(k1 n2) at k1*256 + n2 (column pass of the packed FFT).
@@ -33,7 +44,10 @@ import numpy as np
 
 N = 65536
 L = N // 2
-FSTRIDE = L + 64            # complex elements per row of the half-spectrum buffer
+FSTRIDE = L + 64            # complex elements per half-spectrum plane (>= L + 1)
+OVF_CAP = 1024              # bins with more than two contributing taps, per table
+FROW = 2 * FSTRIDE + 2 * OVF_CAP   # complex elements per batch row of F
+MASK_WORDS = (L + 1 + 31) // 32
 POINTS_PER_TASK = 2048      # 128 threads x 16 values per band workgroup
 STAGE_ORDER = ((16, 2), (16, 4), (16, 8), (16, 16), (256, 2), (256, 4), (256, 8))
 TW_STAGE_LEN = sum(ns * r for ns, r in STAGE_ORDER)
@@ -141,23 +155,58 @@ def build(groups, nn=N):
     cb = (2.0 / N) * (1.0 - 0.5 * edge)
     route_b = record(Ad32 * cb, gd32 * cb)
 
-    scat = np.zeros((ncoef, 4), dtype=np.int32)
-    scat[:, 0] = pos
-    scat[:, 1] = _bits(gd32)
-    scat[:, 2] = _bits(gd32)
+    scat, ovf = scatter_table(pos, gd32, gd32)
 
     gr = g32 * (N / 2.0) / Mt * (1.0 + edge)
     gi = gr * np.where(cf, -1.0, 1.0) * (1.0 - edge)
-    scat_a = np.zeros((ncoef, 4), dtype=np.int32)
-    scat_a[:, 0] = k
-    scat_a[:, 1] = _bits(gr)
-    scat_a[:, 2] = _bits(gi)
+    scat_a, ovf_a = scatter_table(k, gr, gi)
 
     tasks = band_tasks(gspec)
     check_tasks(tasks, ncoef)
     return dict(route=route, route_b=route_b, scat=scat, scat_a=scat_a, tasks=tasks,
+                ovf_scat=ovf, ovf_scat_a=ovf_a,
                 tw_pass=pass_twiddles(), tw_half=half_twiddles(), tw_stage=stage_twiddles(),
                 gspec=gspec, ncoef=ncoef)
+
+
+def scatter_table(bins, gr, gi):
+    """Slot-assigned scatter records {target, gr, gi, 0} and the overflow map.
+
+    Live taps (gr or gi nonzero) are ranked per bin in coefficient order;
+    target = rank * FSTRIDE + bin for ranks 0-1, and
+    2 FSTRIDE + 2 * overflow_index(bin) + rank - 2 for ranks 2-3."""
+    bins = np.asarray(bins, dtype=np.int64)
+    n = bins.size
+    live = (np.asarray(gr) != 0) | (np.asarray(gi) != 0)
+    order = np.lexsort((np.arange(n), bins))          # by bin, then tap index
+    order = order[live[order]]
+    sb = bins[order]
+    first = np.ones(sb.size, dtype=bool)
+    first[1:] = sb[1:] != sb[:-1]
+    start = np.flatnonzero(first)
+    run = np.cumsum(first) - 1
+    rank = np.arange(sb.size) - start[run]
+    deg = np.bincount(bins[live], minlength=L + 1)
+    assert rank.max() <= 3, "more than four taps on one bin"
+    obins = np.flatnonzero(deg > 2)
+    assert obins.size <= OVF_CAP, "overflow area too small"
+    oidx = np.full(L + 1, -1, dtype=np.int64)
+    oidx[obins] = np.arange(obins.size)
+    target = np.zeros(n, dtype=np.int64)
+    tl = np.where(rank < 2, rank * FSTRIDE + sb, 2 * FSTRIDE + 2 * oidx[sb] + (rank - 2))
+    target[order] = tl
+    assert target.max() < FROW
+    rec = np.zeros((n, 4), dtype=np.int32)
+    rec[:, 0] = target
+    rec[:, 1] = _bits(np.where(live, gr, 0.0))
+    rec[:, 2] = _bits(np.where(live, gi, 0.0))
+    mask = np.zeros(MASK_WORDS * 32, dtype=np.uint64)
+    mask[obins] = 1
+    words = (mask.reshape(MASK_WORDS, 32) << np.arange(32, dtype=np.uint64)).sum(1)
+    counts = mask.reshape(MASK_WORDS, 32).sum(1).astype(np.int64)
+    prefix = np.concatenate(([0], np.cumsum(counts)[:-1]))
+    ovf = np.concatenate([words.astype(np.uint32).view(np.int32), prefix.astype(np.int32)])
+    return rec, ovf
 
 
 def check_tasks(tasks, ncoef, points=POINTS_PER_TASK):

@@ -18,6 +18,7 @@
  *   - Return value: FCQT_OK (0), or an FCQT_E* code. Argument errors are
  *     detected before any HIP call is made.
  *   - Calls that share a workspace must be ordered on one stream.
+ *   - Results are deterministic: no kernel uses atomics.
  *
  * Fixed geometry (the reference's fused path hard-requires it,
  * fused.py:230): N = 65536 real samples per slice, L = N/2 = 32768.
@@ -36,7 +37,10 @@ extern "C" {
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
-#define FCQT_FSTRIDE 32832    /* complex elements per batch row of the half-spectrum buffer F (>= L+1) */
+#define FCQT_FSTRIDE 32832    /* complex elements per half-spectrum plane (>= L+1) */
+#define FCQT_OVF_CAP 1024     /* overflow bins (more than two taps) per scatter table */
+#define FCQT_FROW 67712       /* complex elements per batch row of F: 2 planes + 2 x FCQT_OVF_CAP slots */
+#define FCQT_OVF_LEN 2050     /* int32 entries of a scatter table's overflow map */
 #define FCQT_TW_STAGE_LEN 4064 /* complex elements of the stage twiddle table */
 #define FCQT_TW_PASS_LEN 32768 /* complex elements of the pass twiddle table [128][256] */
 #define FCQT_TW_HALF_LEN 32768 /* complex elements of the retangle twiddle table W_65536^i */
@@ -94,29 +98,34 @@ int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* 
                      float* coef_re, float* coef_im, int layout,
                      int64_t batch, hipStream_t stream);
 
-/* Band DFTs + per-tap gain + scatter-add into the half spectrum F:
- *   D_b = DFT_{M_b}(C_b);  F[pos_j] += (gr_j Re D_b[j], gi_j Im D_b[j])
- * with one 16-byte record {pos, gr, gi, 0} per tap; gr = gi = 0 skips a tap.
+/* Band DFTs + per-tap gain + scatter into the half spectrum F:
+ *   D_b = DFT_{M_b}(C_b);  slot(j) of F <- (gr_j Re D_b[j], gi_j Im D_b[j])
+ * with one 16-byte record {slot, gr, gi, 0} per tap; gr = gi = 0 skips a tap.
+ * F holds, per batch row, two planes of FCQT_FSTRIDE bins and an overflow
+ * area of 2 x FCQT_OVF_CAP slots; a bin's value is the sum of its slots. The
+ * table gives every live tap its own slot (no atomics: results are bitwise
+ * reproducible), and the set of slots it writes is fixed, so
+ *   - f must be zero-filled once when allocated (fcqt_fill_zero),
+ *   - a given F buffer must only ever be used with one scatter table.
  * With the synthesis table this is the synthesis front half; with the
  * analysis-adjoint table it is the analysis adjoint front half.
- *   f  [batch][FCQT_FSTRIDE] complex accumulator; MUST be zero on entry
- *      (fcqt_fill_zero once; fcqt_packed_fft_inv re-zeroes it).
- * Uses fp32 atomics: the summation order of overlapping taps (at most 3 per
- * bin) is not fixed, so results may differ in the last bits between runs.
+ *   f  [batch][FCQT_FROW] complex, 16-byte aligned
  * Replaces inv_bands (radix.cu:64-91) and adj_bands (radix.cu:93-114). */
 int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat,
                        const float* coef_re, const float* coef_im, int layout,
                        float* f, int64_t batch, hipStream_t stream);
 
-/* Packed inverse real FFT: y = irfft_65536(F[0..32768]) (imaginary parts of
- * bins 0 and 32768 ignored, as irfft does), then F is reset to zero.
- *   f    [batch][FCQT_FSTRIDE] complex, in; zero on return
+/* Packed inverse real FFT: y = irfft_65536(F[0..32768]) where each bin of F
+ * is the sum of its scatter slots (imaginary parts of bins 0 and 32768
+ * ignored, as irfft does). F is read only.
+ *   ovf  [FCQT_OVF_LEN] int32 overflow map of the scatter table that filled F
+ *   f    [batch][FCQT_FROW] complex
  *   y    [batch][65536] fp32 out (8-byte aligned)
  *   work [batch][32768] complex scratch
- * Replaces inv_tail (packedfft.cu:233-254) and the F memsets
- * (trainable.py:104-105). */
-int fcqt_packed_fft_inv(const fcqt_tables* tab, float* f, float* y, float* work,
-                        int64_t batch, hipStream_t stream);
+ * Replaces inv_tail (packedfft.cu:233-254); the F memsets of the reference
+ * (trainable.py:104-105) are not needed. */
+int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float* f, float* y,
+                        float* work, int64_t batch, hipStream_t stream);
 
 /* Analysis in one call: fcqt_packed_fft_fwd then fcqt_route_bands.
  * z and work are [batch][32768] complex scratch. */
@@ -124,9 +133,9 @@ int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                   float* coef_re, float* coef_im, int layout,
                   float* z, float* work, int64_t batch, hipStream_t stream);
 
-/* Synthesis in one call: fcqt_scatter_bands then fcqt_packed_fft_inv.
- * f must be zero on entry and is zero on return. */
-int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat,
+/* Synthesis in one call: fcqt_scatter_bands then fcqt_packed_fft_inv, with
+ * the scatter table `scat` and its overflow map `ovf` (same F rules). */
+int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* ovf,
                    const float* coef_re, const float* coef_im, int layout,
                    float* f, float* work, float* y, int64_t batch, hipStream_t stream);
 

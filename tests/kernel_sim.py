@@ -175,8 +175,21 @@ def _row_pass(Y, inverse):
     return out
 
 
-def packed_fft_inv(F):
-    """Retangle column pass + row pass: F [B, L+1] -> y [B, N]."""
+def load_bins(Fs, ovf, i):
+    """Value of bins i from the slot buffer Fs [FROW] (packed_fft.hip load_bin)."""
+    v = Fs[i] + Fs[T.FSTRIDE + i]
+    w = ovf[i >> 5].view(np.uint32).astype(np.int64)
+    bit = (w >> (i & 31)) & 1
+    k = ovf[T.MASK_WORDS + (i >> 5)] + np.array([bin(int(x) & ((1 << int(b)) - 1)).count("1")
+                                                 for x, b in zip(w.reshape(-1), (i & 31).reshape(-1))]).reshape(i.shape)
+    k = np.minimum(k, T.OVF_CAP - 1)
+    o = 2 * T.FSTRIDE + 2 * k
+    return np.where(bit == 1, v + Fs[o] + Fs[o + 1], v)
+
+
+def packed_fft_inv(F, ovf=None):
+    """Retangle column pass + row pass -> y [B, N]. F is either a plain half
+    spectrum [B, L+1] or, with ovf, the slot buffer [B, FROW]."""
     F = np.asarray(F, dtype=np.complex128)
     B = F.shape[0]
     twn = T.half_twiddles()
@@ -187,13 +200,14 @@ def packed_fft_inv(F):
     c = np.arange(16)
     tt = np.arange(8)
     for b in range(B):
+        get = (lambda i: F[b][i]) if ovf is None else (lambda i: load_bins(F[b], ovf, i))
         for cg in range(16):
             n2 = cg * 16 + c
             v = np.empty((16, 8, 16), dtype=np.complex128)
             for r in range(16):
                 i = 256 * (tt[None, :] + 8 * r) + n2[:, None]
-                f0 = F[b][i].copy()
-                f1 = F[b][L - i].copy()
+                f0 = get(i).copy()
+                f1 = get(L - i).copy()
                 zero = i == 0
                 f0[zero] = f0[zero].real
                 f1[zero] = f1[zero].real
@@ -255,10 +269,11 @@ def route_bands(Z, route, tasks, ncoef):
 
 
 def scatter_bands(C, scat, tasks, ncoef):
-    """bands.hip scatter_band: C [B, ncoef] -> F [B, L+1] accumulated."""
+    """bands.hip scatter_band: C [B, ncoef] -> slot buffer [B, FROW]; asserts
+    that no slot is written twice."""
     B = C.shape[0]
-    F = np.zeros((B, L + 1), dtype=np.complex128)
-    pos, gr, gi, _ = _decode(scat)
+    F = np.zeros((B, T.FROW), dtype=np.complex128)
+    target, gr, gi, _ = _decode(scat)
     for M, first, nb, _ in tasks.tolist():
         P = Plan(M)
         U = T.POINTS_PER_TASK // M
@@ -276,6 +291,8 @@ def scatter_bands(C, scat, tasks, ncoef):
                 j = (cb + oi).reshape(-1)
                 d = v[u].reshape(-1)
                 live = (gr[j] != 0) | (gi[j] != 0)
-                p = np.minimum(pos[j], L)
-                np.add.at(F[b], p[live], gr[j][live] * d[live].real + 1j * gi[j][live] * d[live].imag)
+                slot = np.minimum(target[j], T.FROW - 1)[live]
+                F[b][slot] = gr[j][live] * d[live].real + 1j * gi[j][live] * d[live].imag
+    tl = target[(gr != 0) | (gi != 0)]
+    assert np.unique(tl).size == tl.size, "two taps share a slot"
     return F

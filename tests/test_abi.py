@@ -61,9 +61,11 @@ def test_argument_errors_detected_before_any_launch(lib):
     assert lib.fcqt_route_bands(ctypes.byref(tab), p, p, p, null, 0, 1, s) == EARG
     assert lib.fcqt_route_bands(ctypes.byref(tab), odd, p, p, p, 0, 1, s) == EALIGN
     assert lib.fcqt_scatter_bands(ctypes.byref(tab), p, p, p, 0, null, 1, s) == EARG
-    assert lib.fcqt_packed_fft_inv(ctypes.byref(tab), p, p, p, -3, s) == EARG
+    assert lib.fcqt_packed_fft_inv(ctypes.byref(tab), p, p, p, p, -3, s) == EARG
+    assert lib.fcqt_packed_fft_inv(ctypes.byref(tab), null, p, p, p, 1, s) == EARG
     assert lib.fcqt_analysis(ctypes.byref(tab), null, p, p, p, 0, p, p, 1, s) == EARG
-    assert lib.fcqt_synthesis(ctypes.byref(tab), p, p, p, 0, odd, p, p, 1, s) == EALIGN
+    assert lib.fcqt_synthesis(ctypes.byref(tab), p, p, p, p, 0, odd, p, p, 1, s) == EALIGN
+    assert lib.fcqt_synthesis(ctypes.byref(tab), p, null, p, p, 0, p, p, p, 1, s) == EARG
     assert lib.fcqt_fill_zero(null, 10, s) == EARG
     assert lib.fcqt_fill_zero(p, 0, s) == 0  # nothing to do, no launch
 

@@ -3,8 +3,8 @@
 Thresholds (north star): forward coefficients >= 120 dB, round trip >= 125
 dB, gradients >= 120 dB, all as 10 log10(|ref|^2 / |ref - got|^2) over the
 whole tensor. The analysis path has no atomics, so its results are bitwise
-reproducible and batch-size independent; the synthesis scatter uses fp32
-atomics (order of at most three overlapping taps per bin may vary).
+reproducible and batch-size independent; the synthesis scatter writes each
+tap to its own slot (no atomics), so synthesis is bitwise reproducible too.
 Mirrors the reference's GPU gates: bench/packedfft.py:89-147,
 bench/radix_gpu.py:152-338, bench/autograd_gpu.py:48-117,
 bench/factored_bars.py:141-150, bench/sliced.py:112-135.
@@ -86,18 +86,23 @@ def test_packed_fft_matches_numpy(fused, B):
 
 
 @pytest.mark.parametrize("B", [1, 2])
-def test_inverse_tail_matches_irfft_and_resets_f(fused, B):
+def test_inverse_tail_matches_irfft(fused, B):
+    """Half spectrum split over the two dense slot planes (overflow slots zero)."""
+    from flash_cqt import tables as T
     rs = np.random.RandomState(200 + B)
     F = (rs.standard_normal((B, L + 1)) + 1j * rs.standard_normal((B, L + 1))).astype(np.complex64)
-    w = fused._workspace(B)
-    w["F"][:, :L + 1, 0] = gpu(F.real)
-    w["F"][:, :L + 1, 1] = gpu(F.imag)
+    a = (rs.uniform(size=(B, L + 1))).astype(np.float32)
+    f = torch.zeros(B, T.FROW, 2, device=_dev())
+    f[:, :L + 1, 0] = gpu(F.real * a)
+    f[:, :L + 1, 1] = gpu(F.imag * a)
+    f[:, T.FSTRIDE:T.FSTRIDE + L + 1, 0] = gpu(F.real * (1 - a))
+    f[:, T.FSTRIDE:T.FSTRIDE + L + 1, 1] = gpu(F.imag * (1 - a))
     y = torch.empty(B, N, device=_dev())
-    fused.packed_ifft(w["F"], y, w["W"])
+    w = fused._workspace(B)
+    fused.packed_ifft(f, y, w["W"])
     torch.cuda.synchronize()
     ref = np.fft.irfft(F.astype(np.complex128), n=N, axis=-1)
     assert snr_db(ref, cnp(y)) > 125
-    assert int(torch.count_nonzero(w["F"])) == 0
 
 
 # ------------------------------------------------------------ analysis
@@ -150,6 +155,16 @@ def test_synthesis_matches_oracle(fused, oracle):
     db = snr_db(ref, cnp(y))
     print(f"synthesis vs oracle {db:.2f} dB")
     assert db >= 120
+
+
+def test_synthesis_bitwise_deterministic(fused):
+    rs = np.random.RandomState(31)
+    C = (rs.standard_normal((3, fused.ncoef)) + 1j * rs.standard_normal((3, fused.ncoef))).astype(np.complex64)
+    kr, ki = gpu(C.real), gpu(C.imag)
+    y1 = fused.bwd(kr, ki).clone()
+    y2 = fused.bwd(kr, ki).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
 
 
 def test_round_trip_randn(fused):
@@ -263,7 +278,7 @@ def test_graph_replay_rebuilds_poisoned_outputs(fused):
         out = g(xg)
         torch.cuda.synchronize()
         assert torch.equal(torch.complex(w["KR"], w["KI"]), eager_k)
-        assert snr_db(cnp(eager_y), cnp(out)) > 125
+        assert torch.equal(out, eager_y)
         _ = torch.randn(1000, device=_dev()).sum()  # eager work between replays
 
 

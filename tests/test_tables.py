@@ -74,7 +74,7 @@ def test_schedule_sim_analysis_and_synthesis(factored_tables, oracle):
     Cref = oracle.flatten(obl, osd)
     assert snr_db(Cref, C) > 140
     F = ks.scatter_bands(Cref, t["scat"], t["tasks"], t["ncoef"])
-    y = ks.packed_fft_inv(F)
+    y = ks.packed_fft_inv(F, t["ovf_scat"])
     assert snr_db(oracle.bwd(obl, osd), y) > 140
 
 
@@ -83,7 +83,7 @@ def test_schedule_sim_adjoints(factored_tables, oracle):
     rs = np.random.RandomState(12)
     G = rs.standard_normal((1, t["ncoef"])) + 1j * rs.standard_normal((1, t["ncoef"]))
     F = ks.scatter_bands(G, t["scat_a"], t["tasks"], t["ncoef"])
-    gx = ks.packed_fft_inv(F)
+    gx = ks.packed_fft_inv(F, t["ovf_scat_a"])
     assert snr_db(oracle.fwd_adjoint(*oracle.unflatten(G)), gx) > 140
     u = rs.standard_normal((1, N))
     Zu = ks.packed_fft_fwd(u)
@@ -98,3 +98,22 @@ def test_inverse_tail_drops_edge_imaginary_parts():
     F = rs.standard_normal((1, L + 1)) + 1j * rs.standard_normal((1, L + 1))
     y = ks.packed_fft_inv(F)
     assert snr_db(np.fft.irfft(F, n=N), y) > 140
+
+
+def test_scatter_slots_unique_and_overflow_map(factored_tables):
+    """Every live tap owns one slot; overflow bins match the map; a bin's
+    slots are exactly its live taps."""
+    from flash_cqt import tables as T
+    for name in ("scat", "scat_a"):
+        rec = factored_tables[name]
+        ovf = factored_tables["ovf_" + name]
+        live = (rec[:, 1] != 0) | (rec[:, 2] != 0)
+        tgt = rec[live, 0].astype(np.int64)
+        assert np.unique(tgt).size == tgt.size
+        assert tgt.max() < T.FROW
+        words = ovf[:T.MASK_WORDS].view(np.uint32)
+        flagged = np.flatnonzero(((words[:, None] >> np.arange(32, dtype=np.uint32)) & 1).reshape(-1))
+        n_over = int((tgt >= 2 * T.FSTRIDE).sum())
+        assert n_over >= flagged.size and flagged.size <= T.OVF_CAP
+        prefix = ovf[T.MASK_WORDS:]
+        assert prefix[0] == 0 and (np.diff(prefix) >= 0).all()
