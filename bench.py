@@ -45,8 +45,8 @@ PEAK_GBPS = 8000.0
 # algorithmic bytes per slice (fp32; tables excluded, batch invariant)
 SLICE_RT_BYTES = 2 * 262144 + 2 * 1063936     # x in, coefficients out, coefficients in, y out
 KERNEL_BYTES = {
-    "packed_fft": 262144 + 262144,            # x in, Z out
-    "route_bands": 262144 + 1063936,          # Z in, coefficients out
+    "packed_fft": 262144 + 262152,            # x in, X (L+1 bins) out
+    "route_bands": 262152 + 1063936,          # X in, coefficients out
     "scatter_bands": 1063936 + 262152,        # coefficients in, half spectrum out
     "packed_ifft": 262152 + 262144,           # half spectrum in, y out
 }
@@ -187,11 +187,11 @@ def kernel_timings(f, B, reps):
     kr = torch.empty(B, f.ncoef, device=dev)
     ki = torch.empty(B, f.ncoef, device=dev)
     y = torch.empty(B, N, device=dev)
-    f.packed_fft(x, w["Z"], w["W"])
-    f.route_bands(w["Z"], kr, ki, _native.PLANAR)
+    f.packed_fft(x, w["X"], w["W"])
+    f.route_bands(w["X"], kr, ki, _native.PLANAR)
     calls = {
-        "packed_fft": lambda: f.packed_fft(x, w["Z"], w["W"]),
-        "route_bands": lambda: f.route_bands(w["Z"], kr, ki, _native.PLANAR),
+        "packed_fft": lambda: f.packed_fft(x, w["X"], w["W"]),
+        "route_bands": lambda: f.route_bands(w["X"], kr, ki, _native.PLANAR),
         "scatter_bands": lambda: f.scatter_bands(kr, ki, _native.PLANAR, w["F"]),
         "packed_ifft": lambda: f.packed_ifft(w["F"], y, w["W"]),
     }
@@ -224,8 +224,8 @@ def kernels_only(f, B, reps):
     src = torch.ones(16 * 1024 * 1024, device=dev)      # 64 MiB
     dst = torch.empty_like(src)
     for _ in range(reps):
-        f.packed_fft(x, w["Z"], w["W"])
-        f.route_bands(w["Z"], kr, ki, _native.PLANAR)
+        f.packed_fft(x, w["X"], w["W"])
+        f.route_bands(w["X"], kr, ki, _native.PLANAR)
         f.scatter_bands(kr, ki, _native.PLANAR, w["F"])
         f.packed_ifft(w["F"], y, w["W"])
         dst.copy_(src)
@@ -277,7 +277,7 @@ def main():
         with torch.no_grad():
             eager = fn().clone()
             g, out = capture(fn)
-            rep_db = replay_matches_eager(g, out, eager, [w["KR"], w["KI"], w["Z"], w["W"], w["XO"]])
+            rep_db = replay_matches_eager(g, out, eager, [w["KR"], w["KI"], w["X"], w["W"], w["XO"]])
             rt_rows = min(snr_db(x[b], eager[b]) for b in range(B))
             KR, KI = f.fwd(x)
             ours = torch.complex(KR, KI).clone()

@@ -8,16 +8,19 @@
 // tasks x batch, spread so that each XCD gets a contiguous range of
 // (task, slice) pairs and so reads each task's record rows from one L2.
 //
-// Analysis prologue (per tap j of a band, one 16-byte record):
-//   v_j = A_j Z[p1_j] + (g_j - A_j) conj Z[p2_j]
-// which is the gather of rfft(x) at the tap's bin times the window (and 1/M)
-// expressed on the packed spectrum Z: X[k] = cA(k) Z[k] + cB(k) conj Z[L-k],
-// cA = (1 - i W_N^k)/2, cB = 1 - cA; conj taps swap the roles.
-// Taps with g = 0 (outside the window support) skip both gathers.
+// Analysis prologue (tap j of a band): v_j = w_j X[k_j], conjugated for taps
+// past Nyquist, where X is the real FFT of the slice (the forward row pass
+// already untangled the packed spectrum) and w_j one fp32 weight per tap
+// (window / M for the analysis, dual window * 2/N for the synthesis
+// adjoint). The bin k_j follows from the band's descriptor {c, r, l}: taps
+// j < r read bin c + j, taps j >= M - l read bin c + j - M (mod N, folded
+// past N/2 to N - k with conjugation), the taps between are zero. The index
+// needs no table, so the weight load and the gather issue together.
 // Synthesis epilogue: tap j stores (gr_j Re D_j, gi_j Im D_j) to its own
-// slot of the half-spectrum buffer F (the record holds the slot target:
+// slot of the half-spectrum buffer F (an 8-byte record holds the slot:
 // plane P0 or P1 at the tap's bin, or an overflow slot for bins with more
-// than two taps); taps with zero gains are skipped. No atomics: each slot has
+// than two taps, the gain gr and how gi follows from it); taps with zero
+// gain are skipped. No atomics: each slot has
 // exactly one writer, so the result is bitwise reproducible, and the
 // inverse column pass sums a bin's slots on load.
 // Reference semantics: radix.cu:46-114, radix_impl.cuh:27-42,100-143.
@@ -51,36 +54,45 @@ __device__ __forceinline__ void store_coef(float* __restrict__ cre, float* __res
 }
 
 template <int M, int LAYOUT>
-__device__ __forceinline__ void route_band(const int4 task, const int b, const float2* __restrict__ z,
+__device__ __forceinline__ void route_band(const int4 task, const int b, const float2* __restrict__ xs,
                                            float* __restrict__ cre, float* __restrict__ cim,
-                                           const int4* __restrict__ route, const long ncoef,
-                                           const float2* __restrict__ tws, float2* lds) {
+                                           const float* __restrict__ wt, const int4* __restrict__ bands,
+                                           const long ncoef, const float2* __restrict__ tws, float2* lds) {
     using P = Plan<M>;
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
     const long cb = (long)task.y + (long)u * M;
-    const float2* zb = z + (long)b * kL;
+    const int4 bd = bands[task.w + (active ? u : 0)];   // {centre bin, r, l, 0}
+    const float2* xb = xs + (long)b * kXStride;
+    // indices first, then every load at once (branch-free, clamped in bounds),
+    // so the 32 loads of a thread are in flight together
+    int kk[16];
+    unsigned live = 0, cj = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int j = t + P::T * r;
+        int k = bd.x + (j < bd.y ? j : j - M);
+        k += k < 0 ? kN : 0;
+        const bool c = k > kL;
+        k = c ? kN - k : k;
+        kk[r] = min(max(k, 0), kL);
+        live |= (active && (j < bd.y || j >= M - bd.z)) ? 1u << r : 0u;
+        cj |= c ? 1u << r : 0u;
+    }
+    const long wb = active ? cb : (long)task.y;
+    float w[16];
+    float2 xv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        w[r] = wt[wb + t + P::T * r];
+        xv[r] = xb[kk[r]];
+    }
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        float2 acc = make_float2(0.0f, 0.0f);
-        if (active) {
-            const int4 rec = route[cb + t + P::T * r];
-            const float g = __int_as_float(rec.w);
-            if (g != 0.0f) {
-                const float ar = __int_as_float(rec.y);
-                const float ai = __int_as_float(rec.z);
-                const int p1 = rec.x & (kL - 1);
-                const int p2 = (int)((unsigned)rec.x >> 16) & (kL - 1);
-                const float2 z1 = zb[p1];
-                const float2 z2 = zb[p2];
-                const float br = g - ar;
-                acc.x = fmaf(ar, z1.x, fmaf(-ai, z1.y, fmaf(br, z2.x, -ai * z2.y)));
-                acc.y = fmaf(ar, z1.y, fmaf(ai, z1.x, fmaf(-ai, z2.x, -br * z2.y)));
-            }
-        }
-        v[r] = acc;
+        const float ww = (live >> r) & 1u ? w[r] : 0.0f;
+        v[r] = make_float2(ww * xv[r].x, (cj >> r) & 1u ? -ww * xv[r].y : ww * xv[r].y);
     }
     fft_unit<M, +1>(v, lds + u * P::US, t, tws);
     if (active) {
@@ -99,7 +111,7 @@ __device__ __forceinline__ void route_band(const int4 task, const int b, const f
 template <int M, int LAYOUT>
 __device__ __forceinline__ void scatter_band(const int4 task, const int b, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
-                                             const int4* __restrict__ scat, const long ncoef,
+                                             const int2* __restrict__ scat, const long ncoef,
                                              const float2* __restrict__ tws, float2* lds) {
     using P = Plan<M>;
     const int u = threadIdx.x / P::T;
@@ -112,19 +124,24 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
     for (int r = 0; r < 16; ++r)
         v[r] = active ? load_coef<LAYOUT>(cre, cim, ib + t + P::T * r) : make_float2(0.0f, 0.0f);
     fft_unit<M, -1>(v, lds + u * P::US, t, tws);
+    // records {slot | mode << 30, gain}: mode 0 gi = gr, 1 gi = -gr, 2 gi = 0;
+    // gain 0 = no slot. All 16 loads issue before the first store.
+    const long rb = active ? cb : (long)task.y;
+    int2 rec[16];
+#pragma unroll
+    for (int q = 0; q < P::QL; ++q)
+#pragma unroll
+        for (int r = 0; r < P::RL; ++r) rec[q * P::RL + r] = scat[rb + t + P::T * q + r * P::OS];
     if (active) {
         float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
 #pragma unroll
-        for (int q = 0; q < P::QL; ++q) {
-#pragma unroll
-            for (int r = 0; r < P::RL; ++r) {
-                const int m = t + P::T * q + r * P::OS;
-                const int4 rec = scat[cb + m];
-                if ((rec.y | rec.z) != 0) {
-                    const unsigned slot = min((unsigned)rec.x, (unsigned)(kFRow - 1));
-                    const float2 d = v[q * P::RL + r];
-                    fb[slot] = make_float2(__int_as_float(rec.y) * d.x, __int_as_float(rec.z) * d.y);
-                }
+        for (int i = 0; i < 16; ++i) {
+            const float gr = __int_as_float(rec[i].y);
+            if (gr != 0.0f) {
+                const unsigned mode = (unsigned)rec[i].x >> 30;
+                const unsigned slot = min((unsigned)rec[i].x & 0x3fffffffu, (unsigned)(kFRow - 1));
+                const float gi = mode == 0 ? gr : (mode == 1 ? -gr : 0.0f);
+                fb[slot] = make_float2(gr * v[i].x, gi * v[i].y);
             }
         }
     }
@@ -137,10 +154,11 @@ __device__ __forceinline__ void decode_task(int batch, int& task, int& b) {
 }
 
 template <int LAYOUT>
-__global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __restrict__ z,
+__global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __restrict__ xs,
                                                               float* __restrict__ cre,
                                                               float* __restrict__ cim,
-                                                              const int4* __restrict__ route,
+                                                              const float* __restrict__ wt,
+                                                              const int4* __restrict__ bands,
                                                               const int4* __restrict__ tasks, int batch,
                                                               long ncoef, const float2* __restrict__ tws) {
     __shared__ float2 lds[kBandLds];
@@ -148,13 +166,13 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
     decode_task(batch, task_id, b);
     const int4 td = tasks[task_id];
     switch (td.x) {
-        case 32: route_band<32, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
-        case 64: route_band<64, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
-        case 128: route_band<128, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
-        case 256: route_band<256, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
-        case 512: route_band<512, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
-        case 1024: route_band<1024, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
-        case 2048: route_band<2048, LAYOUT>(td, b, z, cre, cim, route, ncoef, tws, lds); break;
+        case 32: route_band<32, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
+        case 64: route_band<64, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
+        case 128: route_band<128, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
+        case 256: route_band<256, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
+        case 512: route_band<512, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
+        case 1024: route_band<1024, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
+        case 2048: route_band<2048, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
         default: break;
     }
 }
@@ -163,7 +181,7 @@ template <int LAYOUT>
 __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __restrict__ cre,
                                                                 const float* __restrict__ cim,
                                                                 float* __restrict__ f,
-                                                                const int4* __restrict__ scat,
+                                                                const int2* __restrict__ scat,
                                                                 const int4* __restrict__ tasks, int batch,
                                                                 long ncoef, const float2* __restrict__ tws) {
     __shared__ float2 lds[kBandLds];
@@ -185,11 +203,13 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
 static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const float* cre, const float* cim,
                            int layout, int64_t batch) {
     if (!tab || !rec || !cre || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
-    if (!tab->tasks || !tab->tw_stage || tab->ntasks < 1 || tab->ncoef < 1) return FCQT_EARG;
+    if (!tab->tasks || !tab->bands || !tab->tw_stage || tab->ntasks < 1 || tab->nbands < 1 || tab->ncoef < 1)
+        return FCQT_EARG;
     if ((int64_t)tab->ntasks * batch >= (int64_t)1 << 31) return FCQT_EARG;
     if (layout != FCQT_PLANAR && layout != FCQT_INTERLEAVED) return FCQT_EARG;
     if (layout == FCQT_PLANAR && !cim) return FCQT_EARG;
-    if (!aligned(rec, 16) || !aligned(tab->tasks, 16) || !aligned(tab->tw_stage, 16)) return FCQT_EALIGN;
+    if (!aligned(rec, 4) || !aligned(tab->tasks, 16) || !aligned(tab->bands, 16) || !aligned(tab->tw_stage, 16))
+        return FCQT_EALIGN;
     if (layout == FCQT_PLANAR ? (!aligned(cre, 4) || !aligned(cim, 4)) : !aligned(cre, 8)) return FCQT_EALIGN;
     return FCQT_OK;
 }
@@ -198,23 +218,24 @@ static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const flo
 
 using namespace fcqt;
 
-extern "C" int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* z,
+extern "C" int fcqt_route_bands(const fcqt_tables* tab, const float* weights, const float* xs,
                                 float* coef_re, float* coef_im, int layout, int64_t batch,
                                 hipStream_t stream) {
-    if (int e = check_band_args(tab, route, coef_re, coef_im, layout, batch)) return e;
-    if (!z) return FCQT_EARG;
-    if (!aligned(z, 8)) return FCQT_EALIGN;
+    if (int e = check_band_args(tab, reinterpret_cast<const int32_t*>(weights), coef_re, coef_im, layout, batch))
+        return e;
+    if (!xs) return FCQT_EARG;
+    if (!aligned(xs, 8)) return FCQT_EALIGN;
     const dim3 grid((unsigned)(tab->ntasks * batch));
-    const auto* zz = reinterpret_cast<const float2*>(z);
-    const auto* rr = reinterpret_cast<const int4*>(route);
+    const auto* xx = reinterpret_cast<const float2*>(xs);
+    const auto* bb = reinterpret_cast<const int4*>(tab->bands);
     const auto* tt = reinterpret_cast<const int4*>(tab->tasks);
     const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
     if (layout == FCQT_PLANAR)
-        hipLaunchKernelGGL(k_route_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, zz, coef_re,
-                           coef_im, rr, tt, (int)batch, (long)tab->ncoef, ws);
+        hipLaunchKernelGGL(k_route_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, xx, coef_re,
+                           coef_im, weights, bb, tt, (int)batch, (long)tab->ncoef, ws);
     else
-        hipLaunchKernelGGL(k_route_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream, zz,
-                           coef_re, coef_re, rr, tt, (int)batch, (long)tab->ncoef, ws);
+        hipLaunchKernelGGL(k_route_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream, xx,
+                           coef_re, coef_re, weights, bb, tt, (int)batch, (long)tab->ncoef, ws);
     return launch_status();
 }
 
@@ -223,9 +244,9 @@ extern "C" int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat, c
                                   hipStream_t stream) {
     if (int e = check_band_args(tab, scat, coef_re, coef_im, layout, batch)) return e;
     if (!f) return FCQT_EARG;
-    if (!aligned(f, 16)) return FCQT_EALIGN;
+    if (!aligned(f, 16) || !aligned(scat, 8)) return FCQT_EALIGN;
     const dim3 grid((unsigned)(tab->ntasks * batch));
-    const auto* ss = reinterpret_cast<const int4*>(scat);
+    const auto* ss = reinterpret_cast<const int2*>(scat);
     const auto* tt = reinterpret_cast<const int4*>(tab->tasks);
     const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
     if (layout == FCQT_PLANAR)

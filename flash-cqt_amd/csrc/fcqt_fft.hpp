@@ -32,6 +32,7 @@ constexpr int kFStride = kL + 64;  // complex elements per half-spectrum plane (
 constexpr int kOvfCap = 1024;      // overflow bins (more than two taps) per scatter table
 constexpr int kFRow = 2 * kFStride + 2 * kOvfCap;  // complex elements per batch row of F
 constexpr int kMaskWords = (kL + 1 + 31) / 32;     // overflow bitmask words per table
+constexpr int kXStride = kL + 64;  // complex elements per row of the rfft spectrum X (>= L + 1)
 
 // ------------------------------------------------------------ complex ops
 

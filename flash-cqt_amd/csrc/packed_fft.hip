@@ -1,24 +1,28 @@
-// Packed half-length real FFT of 65536-sample slices, forward and inverse.
-//
-// L = 32768 = 128 x 256 four-step decomposition, n = 256 n1 + n2,
-// k = k1 + 128 k2, in two passes over HBM per direction:
+// Real FFT of 65536-sample slices (forward: rfft, inverse: irfft) as a packed
+// half-length complex FFT, L = 32768 = 128 x 256, four-step decomposition
+// n = 256 n1 + n2, k = k1 + 128 k2, two passes over HBM per direction:
 //   column pass  for each n2: V = DFT_128 over n1, times W_L^{n2 k1},
-//                stored row-major Y[k1][n2] (16 consecutive n2 per workgroup
-//                = 128-byte runs)
-//   row pass     for each k1: DFT_256 over n2 of Y[k1][:], transposed in LDS
-//                and stored at natural index k1 + 128 k2 (16 consecutive k1
-//                per workgroup = 128-byte runs).
+//                stored row-major Y[k1][n2]
+//   row pass     for each k1: DFT_256 over n2 of Y[k1][:], stored at the
+//                natural index k1 + 128 k2.
 // Forward: the column pass reads the real slice as complex pairs
-// z[n] = x[2n] + i x[2n+1] directly (the pack costs nothing).
-// Inverse: the column pass sums each bin's scatter slots (two dense planes
-// plus, for the few bins flagged in the table's overflow bitmask, two
-// overflow slots) and retangles the half spectrum on load,
-//   E = (F[i] + conj F[L-i])/2,  O = (F[i] - conj F[L-i])/2 * conj(W_N^i),
+// z[n] = x[2n] + i x[2n+1] directly; the row pass pairs every row k1 with its
+// mirror row 128 - k1 (rows 0 and 64 are their own mirrors) in one
+// workgroup, so it can untangle on the way out:
+//   X[k] = cA(k) Z[k] + cB(k) conj Z[L-k],  cA = (1 - i W_N^k)/2, cB = 1 - cA,
+// and it writes the real FFT X[0..L] itself (X[L] = Re Z[0] - Im Z[0]).
+// Inverse: the column pass pairs every column n2 with its mirror 256 - n2
+// (columns 0 and 128 are their own mirrors), stages each bin's value (the sum
+// of its scatter slots: two dense planes plus, for bins flagged in the
+// table's overflow map, two overflow slots) in LDS, and retangles there,
+//   E = (F[i] + conj F[L-i])/2,  O = (F[i] - conj F[L-i])/2 conj(W_N^i),
 //   W = conj(E + i O),
-// the row pass runs the same forward FFT and unpacks on store,
-//   y[2k] = Re/L, y[2k+1] = -Im/L.
+// so every bin is read from memory once; the row pass runs the same forward
+// FFT and unpacks on store, y[2k] = Re/L, y[2k+1] = -Im/L.
 // Reference semantics: packedfft.cu:100-169 (three radix-32 passes, separate
-// retangle/unpack launches and a permuted output order there).
+// retangle/unpack launches and a permuted output order there) and the
+// untangle of radix_impl.cuh:27-42, which this engine moves out of the band
+// kernels.
 #include "fcqt_fft.hpp"
 #include "fcqt_abi_internal.hpp"
 
@@ -31,27 +35,27 @@ constexpr int kRowWgs = 128 / kRowsPerWg;      // 8 workgroups per slice
 
 // ------------------------------------------------------------ column pass
 
+// Sum of the two overflow slots of a flagged bin i (mask word w, bit = its bit).
+__device__ __forceinline__ float2 overflow_sum(const float2* __restrict__ fb, const int* __restrict__ ovf, int i,
+                                               unsigned w, unsigned bit) {
+    int k = ovf[kMaskWords + (i >> 5)] + __popc(w & (bit - 1u));
+    k = min(k, kOvfCap - 1);
+    const float2* o = fb + 2 * kFStride + 2 * k;
+    return cadd(o[0], o[1]);
+}
+
 // Value of half-spectrum bin i (0 <= i <= L) from its scatter slots.
 __device__ __forceinline__ float2 load_bin(const float2* __restrict__ fb, const int* __restrict__ ovf, int i) {
     float2 v = cadd(fb[i], fb[kFStride + i]);
     const unsigned w = (unsigned)ovf[i >> 5];
     const unsigned bit = 1u << (i & 31);
-    if (w & bit) {
-        int k = ovf[kMaskWords + (i >> 5)] + __popc(w & (bit - 1u));
-        k = min(k, kOvfCap - 1);
-        const float2* o = fb + 2 * kFStride + 2 * k;
-        v = cadd(v, cadd(o[0], o[1]));
-    }
+    if (w & bit) v = cadd(v, overflow_sum(fb, ovf, i, w, bit));
     return v;
 }
 
-template <bool INVERSE>
-__global__ __launch_bounds__(128) void k_col_pass(const float2* __restrict__ in,
-                                                  float2* __restrict__ out,
-                                                  const float2* __restrict__ twp,
-                                                  const float2* __restrict__ twn,
-                                                  const int* __restrict__ ovf,
-                                                  const float2* __restrict__ tws) {
+__global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, float2* __restrict__ out,
+                                                 const float2* __restrict__ twp,
+                                                 const float2* __restrict__ tws) {
     using P = Plan<128>;
     __shared__ float2 lds[kColsPerWg * P::US];
     const int b = blockIdx.x / kColWgs;
@@ -60,27 +64,9 @@ __global__ __launch_bounds__(128) void k_col_pass(const float2* __restrict__ in,
     const int t = threadIdx.x >> 4;                // thread within the column FFT, < 8
     const int n2 = cg * kColsPerWg + c;
     float2 v[16];
-    if constexpr (!INVERSE) {
-        const float2* xb = in + (long)b * kL;
+    const float2* xb = in + (long)b * kL;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
-    } else {
-        const float2* fb = in + (long)b * kFRow;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 256 * (t + 8 * r) + n2;
-            float2 f0 = load_bin(fb, ovf, i);
-            float2 f1 = load_bin(fb, ovf, kL - i);
-            if (i == 0) {  // bins 0 and L are real for irfft
-                f0.y = 0.0f;
-                f1.y = 0.0f;
-            }
-            const float2 e = make_float2(0.5f * (f0.x + f1.x), 0.5f * (f0.y - f1.y));
-            const float2 d = make_float2(0.5f * (f0.x - f1.x), 0.5f * (f0.y + f1.y));
-            const float2 o = cmulc(d, twn[i]);
-            v[r] = make_float2(e.x - o.y, -(e.y + o.x));
-        }
-    }
+    for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
     fft_unit<128, -1>(v, lds + c * P::US, t, tws);
     // v[q*8 + r] = V[k1], k1 = t + 8 q + 16 r
     float2* yb = out + (long)b * kL;
@@ -95,51 +81,172 @@ __global__ __launch_bounds__(128) void k_col_pass(const float2* __restrict__ in,
     }
 }
 
-// --------------------------------------------------------------- row pass
+// Column of local slot c in inverse column workgroup w: slots 0-7 hold
+// columns p = 8w..8w+7, slots 8-15 their mirrors 256 - p; pair p = 0 is
+// {0, 128} (both self-mirrored).
+__device__ __forceinline__ int inv_col(int w, int c) {
+    const int p = 8 * w + (c & 7);
+    return c < 8 ? p : (p == 0 ? 128 : 256 - p);
+}
 
-template <bool INVERSE>
-__global__ __launch_bounds__(256) void k_row_pass(const float2* __restrict__ in,
-                                                  float2* __restrict__ out,
-                                                  const float2* __restrict__ tws) {
-    using P = Plan<256>;
-    __shared__ float2 lds[kRowsPerWg * P::US];
-    const int b = blockIdx.x / kRowWgs;
-    const int rg = blockIdx.x - b * kRowWgs;
-    const int rho = threadIdx.x >> 4;   // row within the tile
-    const int t = threadIdx.x & 15;     // thread within the row FFT
-    const int k1 = rg * kRowsPerWg + rho;
-    const float2* yb = in + (long)b * kL + (long)k1 * 256;
+__global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, float2* __restrict__ out,
+                                                 const float2* __restrict__ twp,
+                                                 const float2* __restrict__ twn,
+                                                 const int* __restrict__ ovf,
+                                                 const float2* __restrict__ tws) {
+    using P = Plan<128>;
+    __shared__ float2 lds[kColsPerWg * P::US + 1];  // staged bins, then FFT exchange
+    const int b = blockIdx.x / kColWgs;
+    const int w = blockIdx.x - b * kColWgs;
+    const int c = threadIdx.x & (kColsPerWg - 1);
+    const int t = threadIdx.x >> 4;
+    const int col = inv_col(w, c);
+    const float2* fb = f + (long)b * kFRow;
+    float2* raw = lds + c * P::US;
+    {
+        // both dense planes and the overflow mask word of all 16 bins in one
+        // batch of loads; the rare overflow slots are added afterwards
+        float2 p0[16], p1[16];
+        unsigned mw[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 256 * (t + 8 * r) + col;
+            p0[r] = fb[i];
+            p1[r] = fb[kFStride + i];
+            mw[r] = (unsigned)ovf[i >> 5];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 256 * (t + 8 * r) + col;
+            float2 val = cadd(p0[r], p1[r]);
+            const unsigned bit = 1u << (i & 31);
+            if (mw[r] & bit) val = cadd(val, overflow_sum(fb, ovf, i, mw[r], bit));
+            raw[t + 8 * r] = val;
+        }
+    }
+    if (threadIdx.x == 0) lds[kColsPerWg * P::US] = load_bin(fb, ovf, kL);
+    __syncthreads();
+    const float2* mraw = lds + (c ^ 8) * P::US;  // mirror column's bins
     float2 v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = yb[t + 16 * r];
+    for (int r = 0; r < 16; ++r) {
+        const int n1 = t + 8 * r;
+        const int i = 256 * n1 + col;
+        float2 f0 = raw[n1];
+        float2 f1;
+        if (col == 0) f1 = n1 == 0 ? lds[kColsPerWg * P::US] : raw[128 - n1];
+        else if (col == 128) f1 = raw[127 - n1];
+        else f1 = mraw[127 - n1];
+        if (i == 0) {  // bins 0 and L are real for irfft
+            f0.y = 0.0f;
+            f1.y = 0.0f;
+        }
+        const float2 e = make_float2(0.5f * (f0.x + f1.x), 0.5f * (f0.y - f1.y));
+        const float2 d = make_float2(0.5f * (f0.x - f1.x), 0.5f * (f0.y + f1.y));
+        const float2 o = cmulc(d, twn[i]);
+        v[r] = make_float2(e.x - o.y, -(e.y + o.x));
+    }
+    __syncthreads();  // staged bins fully consumed before the FFT reuses LDS
+    fft_unit<128, -1>(v, lds + c * P::US, t, tws);
+    float2* yb = out + (long)b * kL;
+#pragma unroll
+    for (int q = 0; q < P::QL; ++q) {
+#pragma unroll
+        for (int r = 0; r < P::RL; ++r) {
+            const int k1 = t + 8 * q + 16 * r;
+            const int o = k1 * 256 + col;
+            yb[o] = cmul(v[q * P::RL + r], twp[o]);
+        }
+    }
+}
+
+// --------------------------------------------------------------- row pass
+
+// Row of local slot rho in forward row workgroup w: slots 0-7 hold rows
+// p = 8w..8w+7, slots 8-15 their mirrors 128 - p; pair p = 0 is {0, 64}
+// (both self-mirrored).
+__device__ __forceinline__ int fwd_row(int w, int rho) {
+    const int p = 8 * w + (rho & 7);
+    return rho < 8 ? p : (p == 0 ? 64 : 128 - p);
+}
+
+// Row FFTs of one 16-row tile, results left in LDS as Z_row[k2] at
+// lds[rho*US + pad16(k2)] (a barrier follows).
+__device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, float2* lds, int rho, int t,
+                                               const float2* __restrict__ tws) {
+    using P = Plan<256>;
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = yrow[t + 16 * r];
     float2* s = lds + rho * P::US;
     fft_unit<256, -1>(v, s, t, tws);
-    // v[r] = X_row[k2], k2 = t + 16 r ; transpose through LDS so that lanes
-    // walk consecutive k1 for the store at k1 + 128 k2.
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[pad16(t + 16 * r)] = v[r];
     __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, float2* __restrict__ xs,
+                                                 const float2* __restrict__ twn,
+                                                 const float2* __restrict__ tws) {
+    using P = Plan<256>;
+    __shared__ float2 lds[kRowsPerWg * P::US];
+    const int b = blockIdx.x / kRowWgs;
+    const int w = blockIdx.x - b * kRowWgs;
+    const int rho = threadIdx.x >> 4;
+    const int t = threadIdx.x & 15;
+    // untangle twiddles of this thread's output bins, loaded up front
+    const int rho2 = threadIdx.x & 15;
+    const int kg = threadIdx.x >> 4;
+    const int k1 = fwd_row(w, rho2);
+    float2 wn[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) wn[u] = twn[k1 + 128 * (kg + 16 * u)];
+    row_fft_to_lds(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, rho, t, tws);
+    // untangle: lanes walk the tile's rows for coalesced stores
+    const float2* s = lds + rho2 * P::US;
+    const float2* sm = lds + (rho2 ^ 8) * P::US;   // mirror row (rows 0 / 64: own row)
+    float2* xb = xs + (long)b * kXStride;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int k2 = kg + 16 * u;
+        const int k = k1 + 128 * k2;
+        const float2 z = s[pad16(k2)];
+        float2 zm;
+        if (k1 == 0) zm = s[pad16((256 - k2) & 255)];
+        else if (k1 == 64) zm = s[pad16(255 - k2)];
+        else zm = sm[pad16(255 - k2)];
+        // W = W_N^k; cA = (1 + Im W, -Re W)/2, cB = (1 - Im W, Re W)/2, X = cA z + cB conj(zm)
+        const float2 ca = make_float2(0.5f * (1.0f + wn[u].y), -0.5f * wn[u].x);
+        const float2 cb = make_float2(0.5f * (1.0f - wn[u].y), 0.5f * wn[u].x);
+        xb[k] = cadd(cmul(ca, z), cmulc(cb, zm));
+    }
+    if (w == 0 && threadIdx.x == 0) {               // Nyquist bin from Z[0] (row 0, k2 = 0)
+        const float2 z0 = lds[pad16(0)];
+        xb[kL] = make_float2(z0.x - z0.y, 0.0f);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, float2* __restrict__ y,
+                                                 const float2* __restrict__ tws) {
+    using P = Plan<256>;
+    __shared__ float2 lds[kRowsPerWg * P::US];
+    const int b = blockIdx.x / kRowWgs;
+    const int rg = blockIdx.x - b * kRowWgs;
+    const int rho = threadIdx.x >> 4;
+    const int t = threadIdx.x & 15;
+    row_fft_to_lds(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, rho, t, tws);
     const int rho2 = threadIdx.x & 15;
     const int kg = threadIdx.x >> 4;
     const float2* s2 = lds + rho2 * P::US;
     const int kk1 = rg * kRowsPerWg + rho2;
-    if constexpr (!INVERSE) {
-        float2* zb = out + (long)b * kL;
+    constexpr float sc = 1.0f / (float)kL;
+    float2* yo = y + (long)b * kL;  // y viewed as [batch][32768] float pairs
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int k2 = kg + 16 * u;
-            zb[kk1 + 128 * k2] = s2[pad16(k2)];
-        }
-    } else {
-        constexpr float sc = 1.0f / (float)kL;
-        float2* yo = out + (long)b * kL;  // y viewed as [batch][32768] float pairs
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int k2 = kg + 16 * u;
-            const float2 w = s2[pad16(k2)];
-            yo[kk1 + 128 * k2] = make_float2(w.x * sc, -w.y * sc);
-        }
+    for (int u = 0; u < 16; ++u) {
+        const int k2 = kg + 16 * u;
+        const float2 w = s2[pad16(k2)];
+        yo[kk1 + 128 * k2] = make_float2(w.x * sc, -w.y * sc);
     }
 }
 
@@ -147,20 +254,21 @@ __global__ __launch_bounds__(256) void k_row_pass(const float2* __restrict__ in,
 
 using namespace fcqt;
 
-extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* z, float* work,
+extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* xs, float* work,
                                    int64_t batch, hipStream_t stream) {
-    if (!tab || !x || !z || !work || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
-    if (!tab->tw_pass || !tab->tw_stage) return FCQT_EARG;
-    if (!aligned(x, 8) || !aligned(z, 8) || !aligned(work, 8) || !aligned(tab->tw_pass, 8) ||
-        !aligned(tab->tw_stage, 16))
+    if (!tab || !x || !xs || !work || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
+    if (!tab->tw_pass || !tab->tw_half || !tab->tw_stage) return FCQT_EARG;
+    if (!aligned(x, 8) || !aligned(xs, 8) || !aligned(work, 8) || !aligned(tab->tw_pass, 8) ||
+        !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
         return FCQT_EALIGN;
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
-    hipLaunchKernelGGL(k_col_pass<false>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
+    hipLaunchKernelGGL(k_col_fwd, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
                        reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
-                       reinterpret_cast<const float2*>(tab->tw_pass), nullptr, nullptr, tws);
+                       reinterpret_cast<const float2*>(tab->tw_pass), tws);
     if (int e = launch_status()) return e;
-    hipLaunchKernelGGL(k_row_pass<false>, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
-                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(z), tws);
+    hipLaunchKernelGGL(k_row_fwd, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
+                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(xs),
+                       reinterpret_cast<const float2*>(tab->tw_half), tws);
     return launch_status();
 }
 
@@ -172,12 +280,12 @@ extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, c
         !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16) || !aligned(ovf, 4))
         return FCQT_EALIGN;
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
-    hipLaunchKernelGGL(k_col_pass<true>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
+    hipLaunchKernelGGL(k_col_inv, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
                        reinterpret_cast<const float2*>(f), reinterpret_cast<float2*>(work),
                        reinterpret_cast<const float2*>(tab->tw_pass),
                        reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const int*>(ovf), tws);
     if (int e = launch_status()) return e;
-    hipLaunchKernelGGL(k_row_pass<true>, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(k_row_inv, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
                        reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(y), tws);
     return launch_status();
 }

@@ -10,7 +10,8 @@ torch.cuda.graph, i.e. hipGraph) records the launches as they are.
 
 Pipeline (all launches on the current stream, no host sync, no allocation
 after the first call for a batch size):
-  analysis   column pass -> row pass -> route + band IDFT      (3 kernels)
+  analysis   column pass -> row pass (untangle: X = rfft(x))
+             -> windowed band gathers + band IDFT              (3 kernels)
   synthesis  band DFT + slot scatter -> column pass (slot sum, retangle)
              -> row pass (unpack)                              (3 kernels)
 No kernel uses atomics: every result is bitwise reproducible.
@@ -56,7 +57,7 @@ class FusedOctCQT:
         self.gspec = built["gspec"]
         self.ncoef = built["ncoef"]
         self.tables = {}
-        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks",
+        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks", "bands",
                      "tw_pass", "tw_half", "tw_stage"):
             self.tables[name] = torch.as_tensor(np.ascontiguousarray(built[name])).to(dev)
         # table bytes per direction (batch invariant, L2/MALL resident at batch)
@@ -64,8 +65,8 @@ class FusedOctCQT:
         tb = self.tables
         self._ct = _native.Tables(
             tw_pass=tb["tw_pass"].data_ptr(), tw_half=tb["tw_half"].data_ptr(),
-            tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(),
-            ntasks=int(tb["tasks"].shape[0]), reserved=0, ncoef=int(self.ncoef))
+            tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(), bands=tb["bands"].data_ptr(),
+            ntasks=int(tb["tasks"].shape[0]), nbands=int(tb["bands"].shape[0]), ncoef=int(self.ncoef))
         self._ws = {}
 
     # ------------------------------------------------------------ buffers
@@ -78,7 +79,7 @@ class FusedOctCQT:
             with torch.cuda.device(self.dev):
                 e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)
                 z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
-                self._ws[B] = dict(Z=e(B, L, 2), W=e(B, L, 2), F=z(B, T.FROW, 2), FA=z(B, T.FROW, 2),
+                self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=z(B, T.FROW, 2), FA=z(B, T.FROW, 2),
                                    KR=z(B, self.ncoef), KI=z(B, self.ncoef), XO=z(B, N))
         return self._ws[B]
 
@@ -122,19 +123,19 @@ class FusedOctCQT:
         self._need(t, B * per_row_bytes, name)
         return B
 
-    def packed_fft(self, x, z, work):
-        """Z = FFT_L(x[0::2] + i x[1::2]) into z [B, L, 2]."""
+    def packed_fft(self, x, xs, work):
+        """X = rfft(x) (bins 0..L) into xs [B, XSTRIDE, 2]."""
         B = self._batch(x, N * 4, "x")
-        self._need(z, B * L * 8, "z")
+        self._need(xs, B * T.XSTRIDE * 8, "xs")
         self._need(work, B * L * 8, "work")
-        _native.check(self.lib.fcqt_packed_fft_fwd(self._ct, _native.ptr(x), _native.ptr(z),
+        _native.check(self.lib.fcqt_packed_fft_fwd(self._ct, _native.ptr(x), _native.ptr(xs),
                                                    _native.ptr(work), B, _native.stream_handle()),
                       "packed_fft_fwd")
 
-    def route_bands(self, z, out_re, out_im, layout, table="route"):
-        B = self._batch(z, L * 8, "z")
+    def route_bands(self, xs, out_re, out_im, layout, table="route"):
+        B = self._batch(xs, T.XSTRIDE * 8, "xs")
         self._need_coef(out_re, out_im, layout, B, "out")
-        _native.check(self.lib.fcqt_route_bands(self._ct, _native.ptr(self.tables[table]), _native.ptr(z),
+        _native.check(self.lib.fcqt_route_bands(self._ct, _native.ptr(self.tables[table]), _native.ptr(xs),
                                                 _native.ptr(out_re), _native.ptr(out_im), layout, B,
                                                 _native.stream_handle()), "route_bands")
 
@@ -161,7 +162,7 @@ class FusedOctCQT:
         w = self._workspace(B)
         _native.check(self.lib.fcqt_analysis(self._ct, _native.ptr(self.tables[table]), _native.ptr(x),
                                              _native.ptr(out_re), _native.ptr(out_im), layout,
-                                             _native.ptr(w["Z"]), _native.ptr(w["W"]), B,
+                                             _native.ptr(w["X"]), _native.ptr(w["W"]), B,
                                              _native.stream_handle()), "analysis")
 
     def synthesis(self, c_re, c_im, layout, y, table="scat"):

@@ -1,21 +1,21 @@
 """Host-side builder of the factored engine's tables (float64 -> fp32).
 
 Everything the kernels need that does not depend on the batch:
-  route    analysis record per tap, 4 x int32:
-             {p1 | p2 << 16, Re A / M, Im A / M, g / M}
-           the kernel computes v = A Z[p1] + (g - A) conj Z[p2] on the packed
-           spectrum Z = FFT_L(x[0::2] + i x[1::2]) (natural order) and then
-           the unscaled inverse DFT of the band. A = g cA(k) with
-           cA = (1 - i W_N^k)/2; conj taps (DC/Nyquist bands past nn/2) use
-           A = g conj cB(k), cB = 1 - cA, and swap p1/p2. The band's 1/M is
-           folded in (exact: M is a power of two).
-  route_b  synthesis-adjoint record, same form with the dual window times
+  route    analysis weight per tap, fp32: window / M. The kernel gathers
+           the real FFT X (computed by the forward passes, untangle included)
+           at the tap's bin, conjugated for taps past nn/2 (DC/Nyquist bands),
+           multiplies by the weight and runs the band's unscaled inverse DFT.
+           The band's 1/M is folded in (exact: M is a power of two).
+  route_b  synthesis-adjoint weight per tap: dual window times
            (2/N)(1 - [k in {0, L}]/2) (the transpose of irfft is (2/N) rfft
            with bins 0 and L halved; the band's transpose of the forward DFT
            is the unscaled inverse DFT).
-  scat     synthesis record per tap {slot target of pos, gdv, gdv, 0}:
+  bands    per band {centre bin c, r, l, 0}: tap j < r reads bin c + j, tap
+           j >= M - l reads bin c + j - M (mod N; bins past N/2 fold to N - k
+           with conjugation), the taps between lie outside the window.
+  scat     synthesis record per tap, 2 x int32 {slot | mode << 30, gain}:
            the half spectrum is F[pos] = sum over taps of gdv DFT(C).
-  scat_a   analysis-adjoint record {slot target of idx, gr, gi, 0} with
+  scat_a   analysis-adjoint record {slot of idx | mode << 30, gr} with
            gr = g (N/2)/M (1 + edge), gi = -+gr (1 - edge): the transpose of
            rfft is (N/2) irfft with bins 0 and L doubled, of a conj tap the
            conjugate, of the band's 1/M inverse DFT the forward DFT / M.
@@ -29,8 +29,8 @@ Everything the kernels need that does not depend on the batch:
            bin 32 w + b as having overflow slots; the second half holds the
            number of overflow bins before word w (the overflow index of a
            bin is that prefix plus the popcount of the lower bits).
-  tasks    band tasks {M, first coefficient, band count, 0}: consecutive
-           bands of one group, at most POINTS / M per task.
+  tasks    band tasks {M, first coefficient, band count, first band}:
+           consecutive bands of one group, at most POINTS / M per task.
   tw_pass  W_L^(k1 n2) at k1*256 + n2 (column pass of the packed FFT).
   tw_half  W_N^i, i < L (retangle of the inverse).
   tw_stage Stockham stage twiddles W_{NS R}^(r k) in [k][r] rows for
@@ -48,6 +48,7 @@ FSTRIDE = L + 64            # complex elements per half-spectrum plane (>= L + 1
 OVF_CAP = 1024              # bins with more than two contributing taps, per table
 FROW = 2 * FSTRIDE + 2 * OVF_CAP   # complex elements per batch row of F
 MASK_WORDS = (L + 1 + 31) // 32
+XSTRIDE = L + 64            # complex elements per row of the real-FFT spectrum X
 POINTS_PER_TASK = 2048      # 128 threads x 16 values per band workgroup
 STAGE_ORDER = ((16, 2), (16, 4), (16, 8), (16, 16), (256, 2), (256, 4), (256, 8))
 TW_STAGE_LEN = sum(ns * r for ns, r in STAGE_ORDER)
@@ -93,12 +94,34 @@ def half_twiddles():
 
 def band_tasks(gspec, points=POINTS_PER_TASK):
     tasks = []
+    band0 = 0
     for b, M, off in gspec:
         assert M in BAND_LENGTHS, f"band length {M} not supported by the engine"
         per = max(1, points // M)
         for first in range(0, b, per):
-            tasks.append([M, off + first * M, min(per, b - first), 0])
+            tasks.append([M, off + first * M, min(per, b - first), band0 + first])
+        band0 += b
     return np.asarray(tasks, dtype=np.int32)
+
+
+def band_descriptors(groups, nn=N):
+    """{c, r, l, 0} per band, recovered from the group gather tables: the
+    live taps j < r hold bins c..c+r-1 (c = the window centre) and the live
+    taps j >= M - l hold bins c-l..c-1 (mod nn)."""
+    rows = []
+    for idx, gv, pos, gdv, conj in groups:
+        b, M = idx.shape
+        unwrapped = np.where(conj, nn - idx, idx)     # bins before the conj fold
+        for i in range(b):
+            live = gv[i] != 0
+            j = np.flatnonzero(live)
+            lo = j[j < M // 2]
+            hi = j[j >= M // 2]
+            r = int(lo.max()) + 1 if lo.size else 0
+            l = int(M - hi.min()) if hi.size else 0
+            c = int(unwrapped[i, 0])
+            rows.append([c, r, l, 0])
+    return np.asarray(rows, dtype=np.int32)
 
 
 def build(groups, nn=N):
@@ -124,36 +147,12 @@ def build(groups, nn=N):
     Mt = np.concatenate([np.full(i.size, i.shape[1], dtype=np.float64) for i, *_ in groups])
     assert k.min() >= 0 and k.max() <= L and pos.min() >= 0 and pos.max() <= L
 
-    W = _unit_roots(k, N)
-    cA = 0.5 * (1.0 - 1j * W)
-    cB = 0.5 * (1.0 + 1j * W)
-    q1 = k % L
-    q2 = (L - k) % L
-    p1 = np.where(cf, q2, q1)
-    p2 = np.where(cf, q1, q2)
-    pp = (p1 | (p2 << 16)).astype(np.int64)
-    pp = np.where(pp >= 2 ** 31, pp - 2 ** 32, pp).astype(np.int32)
     edge = (k == 0) | (k == L)
-
-    def record(a, w):
-        # fp32 rounding of A and the window first, then exact power-of-two scales
-        rec = np.empty((ncoef, 4), dtype=np.int32)
-        rec[:, 0] = pp
-        rec[:, 1] = _bits(a.real)
-        rec[:, 2] = _bits(a.imag)
-        rec[:, 3] = _bits(w)
-        return rec
-
-    A = np.where(cf, g * np.conj(cB), g * cA)
-    A32 = A.astype(np.complex64).astype(np.complex128)
     g32 = g.astype(np.float32).astype(np.float64)
-    route = record(A32 / Mt, g32 / Mt)
-
-    Ad = np.where(cf, gd * np.conj(cB), gd * cA)
-    Ad32 = Ad.astype(np.complex64).astype(np.complex128)
     gd32 = gd.astype(np.float32).astype(np.float64)
-    cb = (2.0 / N) * (1.0 - 0.5 * edge)
-    route_b = record(Ad32 * cb, gd32 * cb)
+    # exact power-of-two scales of the fp32 window values
+    route = (g32 / Mt).astype(np.float32)
+    route_b = (gd32 * (2.0 / N) * (1.0 - 0.5 * edge)).astype(np.float32)
 
     scat, ovf = scatter_table(pos, gd32, gd32)
 
@@ -162,15 +161,18 @@ def build(groups, nn=N):
     scat_a, ovf_a = scatter_table(k, gr, gi)
 
     tasks = band_tasks(gspec)
-    check_tasks(tasks, ncoef)
-    return dict(route=route, route_b=route_b, scat=scat, scat_a=scat_a, tasks=tasks,
+    bands = band_descriptors(groups)
+    check_tasks(tasks, ncoef, bands)
+    check_band_taps(bands, groups)
+    return dict(route=route, route_b=route_b, scat=scat, scat_a=scat_a, tasks=tasks, bands=bands,
                 ovf_scat=ovf, ovf_scat_a=ovf_a,
                 tw_pass=pass_twiddles(), tw_half=half_twiddles(), tw_stage=stage_twiddles(),
                 gspec=gspec, ncoef=ncoef)
 
 
 def scatter_table(bins, gr, gi):
-    """Slot-assigned scatter records {target, gr, gi, 0} and the overflow map.
+    """Slot-assigned scatter records {target | mode << 30, gr} and the overflow map
+    (mode 0: gi = gr, 1: gi = -gr, 2: gi = 0; gr = 0 marks a tap without slot).
 
     Live taps (gr or gi nonzero) are ranked per bin in coefficient order;
     target = rank * FSTRIDE + bin for ranks 0-1, and
@@ -196,10 +198,14 @@ def scatter_table(bins, gr, gi):
     tl = np.where(rank < 2, rank * FSTRIDE + sb, 2 * FSTRIDE + 2 * oidx[sb] + (rank - 2))
     target[order] = tl
     assert target.max() < FROW
-    rec = np.zeros((n, 4), dtype=np.int32)
-    rec[:, 0] = target
-    rec[:, 1] = _bits(np.where(live, gr, 0.0))
-    rec[:, 2] = _bits(np.where(live, gi, 0.0))
+    gr = np.where(live, gr, 0.0)
+    gi = np.where(live, gi, 0.0)
+    mode = np.where(gi == gr, 0, np.where(gi == -gr, 1, 2))
+    assert np.all((mode != 2) | (gi == 0)), "gi must be gr, -gr or 0"
+    assert np.all(~live | (gr != 0)), "a live tap needs a nonzero gr"
+    rec = np.zeros((n, 2), dtype=np.int32)
+    rec[:, 0] = target | (mode << 30)
+    rec[:, 1] = _bits(gr)
     mask = np.zeros(MASK_WORDS * 32, dtype=np.uint64)
     mask[obins] = 1
     words = (mask.reshape(MASK_WORDS, 32) << np.arange(32, dtype=np.uint64)).sum(1)
@@ -209,10 +215,38 @@ def scatter_table(bins, gr, gi):
     return rec, ovf
 
 
-def check_tasks(tasks, ncoef, points=POINTS_PER_TASK):
+def check_tasks(tasks, ncoef, bands, points=POINTS_PER_TASK):
     """Reject a task table the kernels could not execute in bounds."""
     assert tasks.ndim == 2 and tasks.shape[1] == 4 and tasks.shape[0] >= 1
-    for M, first, nb, _ in tasks.tolist():
+    for M, first, nb, band0 in tasks.tolist():
         assert M in BAND_LENGTHS
         assert 1 <= nb <= max(1, points // M)
         assert 0 <= first and first + nb * M <= ncoef
+        assert 0 <= band0 and band0 + nb <= bands.shape[0]
+
+
+def tap_bins(c, r, l, M, nn=N):
+    """Bin and conj flag of every tap j of a band (-1 outside the window),
+    exactly as the band kernel derives them."""
+    j = np.arange(M)
+    live = (j < r) | (j >= M - l)
+    k = c + np.where(j < r, j, j - M)
+    k = np.where(k < 0, k + nn, k)
+    cj = k > nn // 2
+    k = np.where(cj, nn - k, k)
+    return np.where(live, k, -1), cj & live
+
+
+def check_band_taps(bands, groups, nn=N):
+    """The descriptor rule must reproduce the gather table on every live tap."""
+    bi = 0
+    for idx, gv, pos, gdv, conj in groups:
+        b, M = idx.shape
+        for i in range(b):
+            c, r, l, _ = bands[bi].tolist()
+            k, cj = tap_bins(c, r, l, M, nn)
+            live = gv[i] != 0
+            assert np.array_equal(k[live], idx[i][live]), "band descriptor disagrees with the gather table"
+            assert np.array_equal(cj[live], conj[i][live])
+            assert not np.any((k < 0) & live)
+            bi += 1

@@ -2,7 +2,8 @@
  *
  * The library (libflashcqt.so, built with hipcc) implements the hot path of
  * the factored constant-Q transform for 65536-sample slices:
- *   analysis   x -> packed half-length FFT -> route + band inverse DFTs -> C
+ *   analysis   x -> real FFT (packed half-length FFT + untangle) -> windowed
+ *              band gathers + band inverse DFTs -> C
  *   synthesis  C -> band DFTs + gain + scatter -> packed inverse FFT -> y
  * and both adjoints by running the same kernels with different tables.
  *
@@ -33,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 1
+#define FCQT_ABI_VERSION 2
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -41,6 +42,7 @@ extern "C" {
 #define FCQT_OVF_CAP 1024     /* overflow bins (more than two taps) per scatter table */
 #define FCQT_FROW 67712       /* complex elements per batch row of F: 2 planes + 2 x FCQT_OVF_CAP slots */
 #define FCQT_OVF_LEN 2050     /* int32 entries of a scatter table's overflow map */
+#define FCQT_XSTRIDE 32832    /* complex elements per batch row of the real-FFT spectrum X (>= L+1) */
 #define FCQT_TW_STAGE_LEN 4064 /* complex elements of the stage twiddle table */
 #define FCQT_TW_PASS_LEN 32768 /* complex elements of the pass twiddle table [128][256] */
 #define FCQT_TW_HALF_LEN 32768 /* complex elements of the retangle twiddle table W_65536^i */
@@ -60,9 +62,11 @@ typedef struct fcqt_tables {
     const float*   tw_pass;   /* [128][256] complex, W_32768^(k1*n2) at k1*256+n2 */
     const float*   tw_half;   /* [32768] complex, W_65536^i */
     const float*   tw_stage;  /* [FCQT_TW_STAGE_LEN] complex band/pass stage twiddles */
-    const int32_t* tasks;     /* [ntasks][4] band tasks: M, coefficient offset, band count, 0 */
+    const int32_t* tasks;     /* [ntasks][4] band tasks: M, first coefficient, band count, first band */
+    const int32_t* bands;     /* [nbands][4] band descriptors: centre bin c, r, l, 0 (tap j < r reads
+                                 bin c+j, tap j >= M-l reads bin c+j-M, the others are zero) */
     int32_t        ntasks;
-    int32_t        reserved;
+    int32_t        nbands;
     int64_t        ncoef;     /* complex coefficients per slice (132992 for [3,4,2]/[8,16,32]) */
 } fcqt_tables;
 
@@ -75,32 +79,36 @@ const char* fcqt_status_string(int status);
 /* Text of the last HIP error seen by a launcher on this thread ("" if none). */
 const char* fcqt_last_hip_error(void);
 
-/* Packed forward FFT of real slices.
+/* Real FFT of 65536-sample slices as a packed half-length FFT:
  *   x    [batch][65536] fp32 (8-byte aligned)
- *   z    [batch][32768] complex, out: Z = FFT_32768(x[0::2] + i x[1::2]), natural order
+ *   xs   [batch][FCQT_XSTRIDE] complex, out: X = rfft(x), bins 0..32768
  *   work [batch][32768] complex scratch
- * Replaces the even/odd pack copies (trainable.py:81-82) and fft3
- * (packedfft.cu:100-126); two launches (column pass, row pass). */
-int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* z, float* work,
+ * Z = FFT_32768(x[0::2] + i x[1::2]) is untangled on the way out,
+ * X[k] = cA(k) Z[k] + cB(k) conj Z[L-k]. Replaces the even/odd pack copies
+ * (trainable.py:81-82) and fft3 (packedfft.cu:100-126) plus the untangle
+ * the reference does per tap (radix_impl.cuh:27-42); two launches. */
+int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* xs, float* work,
                         int64_t batch, hipStream_t stream);
 
-/* Route + band inverse DFTs: every coefficient c of band b is
- *   C_b[m] = sum_j (A_j Z[p1_j] + (g_j - A_j) conj Z[p2_j]) e^{+2 pi i jm/M_b}
- * with one 16-byte record {p1 | p2<<16, Re A, Im A, g} per tap (the 1/M and
- * every window/untangle constant folded in). With the analysis table this is
- * the analysis; with the dual-window table it is the synthesis adjoint.
- *   z      [batch][32768] complex (from fcqt_packed_fft_fwd)
- *   coef   layout FCQT_PLANAR: coef_re, coef_im [batch][ncoef] fp32
- *          layout FCQT_INTERLEAVED: coef_re is [batch][ncoef] complex, coef_im unused
- *   route  [ncoef][4] int32 records
+/* Windowed band gathers + band inverse DFTs: coefficient m of band b is
+ *   C_b[m] = sum_j w_j X~[k_j] e^{+2 pi i jm/M_b}
+ * where k_j is the tap's bin from the band descriptor and X~ is X, or its
+ * conjugate for taps past N/2 (folded to N - k). One fp32 weight per tap:
+ * window/M gives the analysis, dual window * 2/N (halved at bins 0 and L)
+ * the synthesis adjoint.
+ *   xs      [batch][FCQT_XSTRIDE] complex real-FFT spectrum (fcqt_packed_fft_fwd)
+ *   coef    layout FCQT_PLANAR: coef_re, coef_im [batch][ncoef] fp32
+ *           layout FCQT_INTERLEAVED: coef_re is [batch][ncoef] complex, coef_im unused
+ *   weights [ncoef] fp32
  * Replaces fwd_bands (radix.cu:46-62). */
-int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* z,
+int fcqt_route_bands(const fcqt_tables* tab, const float* weights, const float* xs,
                      float* coef_re, float* coef_im, int layout,
                      int64_t batch, hipStream_t stream);
 
 /* Band DFTs + per-tap gain + scatter into the half spectrum F:
  *   D_b = DFT_{M_b}(C_b);  slot(j) of F <- (gr_j Re D_b[j], gi_j Im D_b[j])
- * with one 16-byte record {slot, gr, gi, 0} per tap; gr = gi = 0 skips a tap.
+ * with one 8-byte record {slot | mode << 30, gr} per tap: gi = gr (mode 0),
+ * -gr (mode 1) or 0 (mode 2); gr = 0 skips a tap.
  * F holds, per batch row, two planes of FCQT_FSTRIDE bins and an overflow
  * area of 2 x FCQT_OVF_CAP slots; a bin's value is the sum of its slots. The
  * table gives every live tap its own slot (no atomics: results are bitwise
@@ -111,7 +119,7 @@ int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* 
  * analysis-adjoint table it is the analysis adjoint front half.
  *   f  [batch][FCQT_FROW] complex, 16-byte aligned
  * Replaces inv_bands (radix.cu:64-91) and adj_bands (radix.cu:93-114). */
-int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat,
+int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat /* [ncoef][2] */,
                        const float* coef_re, const float* coef_im, int layout,
                        float* f, int64_t batch, hipStream_t stream);
 
@@ -128,10 +136,10 @@ int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float*
                         float* work, int64_t batch, hipStream_t stream);
 
 /* Analysis in one call: fcqt_packed_fft_fwd then fcqt_route_bands.
- * z and work are [batch][32768] complex scratch. */
-int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
+ * xs is [batch][FCQT_XSTRIDE] and work [batch][32768] complex scratch. */
+int fcqt_analysis(const fcqt_tables* tab, const float* weights, const float* x,
                   float* coef_re, float* coef_im, int layout,
-                  float* z, float* work, int64_t batch, hipStream_t stream);
+                  float* xs, float* work, int64_t batch, hipStream_t stream);
 
 /* Synthesis in one call: fcqt_scatter_bands then fcqt_packed_fft_inv, with
  * the scatter table `scat` and its overflow map `ovf` (same F rules). */

@@ -125,19 +125,22 @@ def unit_output_index(M):
 
 # ------------------------------------------------------------ packed FFT
 
-def packed_fft_fwd(x):
-    """Column + row pass of packed_fft.hip on x [B, N] -> Z [B, L] natural."""
+def _c(t):
+    return t[:, 0].astype(np.complex128) + 1j * t[:, 1].astype(np.complex128)
+
+
+def col_fwd(x):
+    """k_col_fwd: x [B, N] real -> Y [B, L] (rows k1, columns n2)."""
     x = np.asarray(x, dtype=np.float64)
     B = x.shape[0]
     z = x[:, 0::2] + 1j * x[:, 1::2]
-    twp = T.pass_twiddles()
-    twp = twp[:, 0] + 1j * twp[:, 1]
+    twp = _c(T.pass_twiddles())
     Y = np.empty((B, L), dtype=np.complex128)
     c = np.arange(16)
     tt = np.arange(8)
     for b in range(B):
         for cg in range(16):
-            n2 = cg * 16 + c                                  # [16]
+            n2 = cg * 16 + c
             v = np.empty((16, 8, 16), dtype=np.complex128)    # [unit=c, t, r]
             for r in range(16):
                 idx = 256 * (tt[None, :] + 8 * r) + n2[:, None]
@@ -150,7 +153,56 @@ def packed_fft_fwd(x):
                     o = k1[None, :] * 256 + n2[:, None]
                     assert o.max() < L
                     Y[b][o] = v[:, :, q * 8 + r] * twp[o]
-    return _row_pass(Y, inverse=False)
+    return Y
+
+
+def fwd_row(w, rho):
+    p = 8 * w + (rho & 7)
+    return p if rho < 8 else (64 if p == 0 else 128 - p)
+
+
+def row_fwd(Y):
+    """k_row_fwd: paired row FFTs + untangle -> X [B, L+1] (rfft)."""
+    B = Y.shape[0]
+    twn = _c(T.half_twiddles())
+    X = np.full((B, L + 1), np.nan + 0j)
+    t = np.arange(16)
+    for b in range(B):
+        for w in range(8):
+            rows = np.array([fwd_row(w, rho) for rho in range(16)])
+            v = np.empty((16, 16, 16), dtype=np.complex128)
+            for r in range(16):
+                v[:, :, r] = Y[b][rows[:, None] * 256 + (t[None, :] + 16 * r)]
+            v = fft_unit(v, 256, -1)
+            Zr = np.empty((16, 256), dtype=np.complex128)       # LDS: row rho, column k2
+            for r in range(16):
+                Zr[:, t + 16 * r] = v[:, :, r]
+            for rho2 in range(16):
+                k1 = rows[rho2]
+                k2 = np.arange(256)
+                k = k1 + 128 * k2
+                z = Zr[rho2, k2]
+                if k1 == 0:
+                    zm = Zr[rho2, (256 - k2) & 255]
+                elif k1 == 64:
+                    zm = Zr[rho2, 255 - k2]
+                else:
+                    assert rows[rho2 ^ 8] == 128 - k1
+                    zm = Zr[rho2 ^ 8, 255 - k2]
+                wn = twn[k]
+                ca = 0.5 * (1 + wn.imag) - 0.5j * wn.real
+                cb = 0.5 * (1 - wn.imag) + 0.5j * wn.real
+                X[b][k] = ca * z + cb * np.conj(zm)
+            if w == 0:
+                z0 = Zr[0, 0]
+                X[b][L] = z0.real - z0.imag
+    assert not np.isnan(X).any()
+    return X
+
+
+def packed_fft_fwd(x):
+    """Forward passes of packed_fft.hip: x [B, N] -> X = rfft(x) [B, L+1]."""
+    return row_fwd(col_fwd(x))
 
 
 def _row_pass(Y, inverse):
@@ -187,39 +239,54 @@ def load_bins(Fs, ovf, i):
     return np.where(bit == 1, v + Fs[o] + Fs[o + 1], v)
 
 
+def inv_col(w, c):
+    p = 8 * w + (c & 7)
+    return p if c < 8 else (128 if p == 0 else 256 - p)
+
+
 def packed_fft_inv(F, ovf=None):
-    """Retangle column pass + row pass -> y [B, N]. F is either a plain half
-    spectrum [B, L+1] or, with ovf, the slot buffer [B, FROW]."""
+    """k_col_inv (paired columns, retangle from staged bins) + k_row_inv.
+    F is a plain half spectrum [B, L+1] or, with ovf, the slot buffer [B, FROW]."""
     F = np.asarray(F, dtype=np.complex128)
     B = F.shape[0]
-    twn = T.half_twiddles()
-    twn = twn[:, 0] + 1j * twn[:, 1]
-    twp = T.pass_twiddles()
-    twp = twp[:, 0] + 1j * twp[:, 1]
+    twn = _c(T.half_twiddles())
+    twp = _c(T.pass_twiddles())
     Y = np.empty((B, L), dtype=np.complex128)
-    c = np.arange(16)
     tt = np.arange(8)
+    n1s = np.arange(128)
     for b in range(B):
         get = (lambda i: F[b][i]) if ovf is None else (lambda i: load_bins(F[b], ovf, i))
-        for cg in range(16):
-            n2 = cg * 16 + c
+        nyq = get(np.array([L]))[0]
+        for w in range(16):
+            cols = np.array([inv_col(w, c) for c in range(16)])
+            raw = get(256 * n1s[None, :] + cols[:, None])       # staged [c][n1]
             v = np.empty((16, 8, 16), dtype=np.complex128)
             for r in range(16):
-                i = 256 * (tt[None, :] + 8 * r) + n2[:, None]
-                f0 = get(i).copy()
-                f1 = get(L - i).copy()
-                zero = i == 0
-                f0[zero] = f0[zero].real
-                f1[zero] = f1[zero].real
-                e = 0.5 * (f0 + np.conj(f1))
-                d = 0.5 * (f0 - np.conj(f1))
-                o = d * np.conj(twn[i])
-                v[:, :, r] = np.conj(e + 1j * o)
+                n1 = tt + 8 * r
+                for c in range(16):
+                    col = cols[c]
+                    i = 256 * n1 + col
+                    f0 = raw[c, n1].copy()
+                    if col == 0:
+                        f1 = np.where(n1 == 0, nyq, raw[c, (128 - n1) % 128])
+                    elif col == 128:
+                        f1 = raw[c, 127 - n1]
+                    else:
+                        assert cols[c ^ 8] == 256 - col
+                        f1 = raw[c ^ 8, 127 - n1]
+                    f1 = f1.copy()
+                    zero = i == 0
+                    f0[zero] = f0[zero].real
+                    f1[zero] = f1[zero].real
+                    e = 0.5 * (f0 + np.conj(f1))
+                    d = 0.5 * (f0 - np.conj(f1))
+                    o = d * np.conj(twn[i])
+                    v[c, :, r] = np.conj(e + 1j * o)
             v = fft_unit(v, 128, -1)
             for q in range(2):
                 for r in range(8):
                     k1 = tt + 8 * q + 16 * r
-                    o = k1[None, :] * 256 + n2[:, None]
+                    o = k1[None, :] * 256 + cols[:, None]
                     Y[b][o] = v[:, :, q * 8 + r] * twp[o]
     zp = _row_pass(Y, inverse=True)
     y = np.empty((B, N))
@@ -231,34 +298,37 @@ def packed_fft_inv(F, ovf=None):
 # ----------------------------------------------------------- band engines
 
 def _decode(rec):
-    f = rec.view(np.float32)
-    return rec[:, 0], f[:, 1].astype(np.float64), f[:, 2].astype(np.float64), f[:, 3].astype(np.float64)
+    """8-byte scatter record -> (slot, gr, gi)."""
+    slot = (rec[:, 0].view(np.uint32) & 0x3FFFFFFF).astype(np.int64)
+    mode = rec[:, 0].view(np.uint32) >> 30
+    gr = rec[:, 1].view(np.float32).astype(np.float64)
+    gi = np.where(mode == 0, gr, np.where(mode == 1, -gr, 0.0))
+    return slot, gr, gi
 
 
-def route_bands(Z, route, tasks, ncoef):
-    """bands.hip route_band on Z [B, L] -> coefficients [B, ncoef]."""
-    B = Z.shape[0]
+def route_bands(X, weights, bands, tasks, ncoef):
+    """bands.hip route_band on X [B, L+1] -> coefficients [B, ncoef]."""
+    B = X.shape[0]
     out = np.full((B, ncoef), np.nan + 0j)
-    pp, ar, ai, g = _decode(route)
-    p1 = pp & (L - 1)
-    p2 = (pp.astype(np.int64) >> 16) & (L - 1)
-    A = ar + 1j * ai
-    Bc = (g - ar) - 1j * ai
-    for M, first, nb, _ in tasks.tolist():
+    wt = weights.astype(np.float64)
+    for M, first, nb, band0 in tasks.tolist():
         P = Plan(M)
         U = T.POINTS_PER_TASK // M
-        assert nb <= U
+        assert nb <= U and band0 + nb <= bands.shape[0]
         t = np.arange(P.T)
         for b in range(B):
             v = np.zeros((U, P.T, 16), dtype=np.complex128)
             for u in range(nb):
                 cb = first + u * M
+                c, r_, l_, _ = bands[band0 + u].tolist()
+                k, cj = T.tap_bins(c, r_, l_, M)
+                assert k.max() <= L
                 for r in range(16):
-                    j = cb + t + P.T * r
-                    assert j.max() < ncoef
-                    live = g[j] != 0
-                    val = A[j] * Z[b][p1[j]] + Bc[j] * np.conj(Z[b][p2[j]])
-                    v[u, :, r] = np.where(live, val, 0)
+                    j = t + P.T * r
+                    live = k[j] >= 0
+                    xv = X[b][np.clip(k[j], 0, L)]
+                    xv = np.where(cj[j], np.conj(xv), xv)
+                    v[u, :, r] = np.where(live, wt[cb + j] * xv, 0)
             v = fft_unit(v, M, +1)
             oi = unit_output_index(M)
             for u in range(nb):
@@ -273,7 +343,7 @@ def scatter_bands(C, scat, tasks, ncoef):
     that no slot is written twice."""
     B = C.shape[0]
     F = np.zeros((B, T.FROW), dtype=np.complex128)
-    target, gr, gi, _ = _decode(scat)
+    target, gr, gi = _decode(scat)
     for M, first, nb, _ in tasks.tolist():
         P = Plan(M)
         U = T.POINTS_PER_TASK // M
@@ -290,9 +360,9 @@ def scatter_bands(C, scat, tasks, ncoef):
                 cb = first + u * M
                 j = (cb + oi).reshape(-1)
                 d = v[u].reshape(-1)
-                live = (gr[j] != 0) | (gi[j] != 0)
+                live = gr[j] != 0
                 slot = np.minimum(target[j], T.FROW - 1)[live]
                 F[b][slot] = gr[j][live] * d[live].real + 1j * gi[j][live] * d[live].imag
-    tl = target[(gr != 0) | (gi != 0)]
+    tl = target[gr != 0]
     assert np.unique(tl).size == tl.size, "two taps share a slot"
     return F

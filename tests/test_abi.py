@@ -32,7 +32,8 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fcqt_abi_version() == 1
+    from flash_cqt import _native
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 2
 
 
 def test_status_strings(lib):
@@ -42,8 +43,8 @@ def test_status_strings(lib):
 
 def test_argument_errors_detected_before_any_launch(lib):
     from flash_cqt._native import Tables
-    tab = Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=1, reserved=0, ncoef=1)
-    bad = Tables(tw_pass=0, tw_half=0, tw_stage=0, tasks=0, ntasks=0, reserved=0, ncoef=0)
+    tab = Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, bands=16, ntasks=1, nbands=1, ncoef=1)
+    bad = Tables(tw_pass=0, tw_half=0, tw_stage=0, tasks=0, bands=0, ntasks=0, nbands=0, ncoef=0)
     s = ctypes.c_void_p(0)
     p = ctypes.c_void_p(4096)
     odd = ctypes.c_void_p(4100)
@@ -59,7 +60,8 @@ def test_argument_errors_detected_before_any_launch(lib):
     # bad layout, null im plane for planar
     assert lib.fcqt_route_bands(ctypes.byref(tab), p, p, p, p, 7, 1, s) == EARG
     assert lib.fcqt_route_bands(ctypes.byref(tab), p, p, p, null, 0, 1, s) == EARG
-    assert lib.fcqt_route_bands(ctypes.byref(tab), odd, p, p, p, 0, 1, s) == EALIGN
+    assert lib.fcqt_route_bands(ctypes.byref(tab), ctypes.c_void_p(4098), p, p, p, 0, 1, s) == EALIGN
+    assert lib.fcqt_route_bands(ctypes.byref(bad), p, p, p, p, 0, 1, s) == EARG
     assert lib.fcqt_scatter_bands(ctypes.byref(tab), p, p, p, 0, null, 1, s) == EARG
     assert lib.fcqt_packed_fft_inv(ctypes.byref(tab), p, p, p, p, -3, s) == EARG
     assert lib.fcqt_packed_fft_inv(ctypes.byref(tab), null, p, p, p, 1, s) == EARG

@@ -44,32 +44,30 @@ def test_task_table_covers_every_coefficient_once(factored_tables):
     assert (seen == 1).all()
 
 
-def test_record_fields(factored_tables, pkg_cqt_cpu):
-    """Route records: p1/p2 are the packed-spectrum taps of the gather bin,
-    g is the window / M, and B = g - A reproduces cB g (cA + cB = 1)."""
+def test_weights_and_band_descriptors(factored_tables, pkg_cqt_cpu):
+    """Analysis weights are the fp32 window / M; the band descriptor rule
+    reproduces every live gather index and conj flag of the reference tables;
+    synthesis-adjoint weights are the dual window * 2/N, halved at bins 0, L."""
+    from flash_cqt import tables as T
     t = factored_tables
     groups = pkg_cqt_cpu.np_groups + pkg_cqt_cpu.np_side_groups
-    k = np.concatenate([g[0].reshape(-1) for g in groups])
-    cf = np.concatenate([g[4].reshape(-1) for g in groups])
-    M = np.concatenate([np.full(g[0].size, g[0].shape[1]) for g in groups])
     gv = np.concatenate([g[1].reshape(-1) for g in groups]).astype(np.float64)
-    r = t["route"]
-    p1 = r[:, 0] & 0xFFFF
-    p2 = (r[:, 0] >> 16) & 0xFFFF
-    L = N // 2
-    assert np.array_equal(np.where(cf, (L - k) % L, k % L), p1)
-    assert np.array_equal(np.where(cf, k % L, (L - k) % L), p2)
-    g = r[:, 3].view(np.float32).astype(np.float64)
-    assert np.array_equal(g * M, gv.astype(np.float32).astype(np.float64))
+    gd = np.concatenate([g[3].reshape(-1) for g in groups]).astype(np.float64)
+    k = np.concatenate([g[0].reshape(-1) for g in groups])
+    M = np.concatenate([np.full(g[0].size, g[0].shape[1]) for g in groups])
+    assert np.array_equal(t["route"].astype(np.float64) * M, gv)
+    edge = (k == 0) | (k == N // 2)
+    assert np.array_equal(t["route_b"].astype(np.float64) * (N / 2.0) / (1 - 0.5 * edge), gd)
+    T.check_band_taps(t["bands"], groups)
 
 
 def test_schedule_sim_analysis_and_synthesis(factored_tables, oracle):
     t = factored_tables
     x, _ = inputs()
     x = x[:1].astype(np.float64)
-    Z = ks.packed_fft_fwd(x)
-    assert snr_db(np.fft.fft(x[:, 0::2] + 1j * x[:, 1::2]), Z) > 140
-    C = ks.route_bands(Z, t["route"], t["tasks"], t["ncoef"])
+    X = ks.packed_fft_fwd(x)
+    assert snr_db(np.fft.rfft(x), X) > 140
+    C = ks.route_bands(X, t["route"], t["bands"], t["tasks"], t["ncoef"])
     obl, osd = oracle.fwd(x)
     Cref = oracle.flatten(obl, osd)
     assert snr_db(Cref, C) > 140
@@ -86,8 +84,8 @@ def test_schedule_sim_adjoints(factored_tables, oracle):
     gx = ks.packed_fft_inv(F, t["ovf_scat_a"])
     assert snr_db(oracle.fwd_adjoint(*oracle.unflatten(G)), gx) > 140
     u = rs.standard_normal((1, N))
-    Zu = ks.packed_fft_fwd(u)
-    gC = ks.route_bands(Zu, t["route_b"], t["tasks"], t["ncoef"])
+    Xu = ks.packed_fft_fwd(u)
+    gC = ks.route_bands(Xu, t["route_b"], t["bands"], t["tasks"], t["ncoef"])
     assert snr_db(oracle.flatten(*oracle.bwd_adjoint(u)), gC) > 140
 
 
@@ -107,8 +105,8 @@ def test_scatter_slots_unique_and_overflow_map(factored_tables):
     for name in ("scat", "scat_a"):
         rec = factored_tables[name]
         ovf = factored_tables["ovf_" + name]
-        live = (rec[:, 1] != 0) | (rec[:, 2] != 0)
-        tgt = rec[live, 0].astype(np.int64)
+        live = rec[:, 1] != 0
+        tgt = (rec[live, 0].view(np.uint32) & 0x3FFFFFFF).astype(np.int64)
         assert np.unique(tgt).size == tgt.size
         assert tgt.max() < T.FROW
         words = ovf[:T.MASK_WORDS].view(np.uint32)
