@@ -13,8 +13,9 @@
 // and it writes the real FFT X[0..L] itself (X[L] = Re Z[0] - Im Z[0]).
 // Inverse: the column pass pairs every column n2 with its mirror 256 - n2
 // (columns 0 and 128 are their own mirrors), stages each bin's value (the sum
-// of its scatter slots: two dense planes plus, for bins flagged in the
-// table's overflow map, two overflow slots) in LDS, and retangles there,
+// of its scatter slots: two dense slots plus, for the bins on the table's
+// overflow fold list of this workgroup, two overflow slots) in LDS, and
+// retangles there,
 //   E = (F[i] + conj F[L-i])/2,  O = (F[i] - conj F[L-i])/2 conj(W_N^i),
 //   W = conj(E + i O),
 // so every bin is read from memory once; the row pass runs the same forward
@@ -35,22 +36,13 @@ constexpr int kRowWgs = 128 / kRowsPerWg;      // 8 workgroups per slice
 
 // ------------------------------------------------------------ column pass
 
-// Sum of the two overflow slots of a flagged bin i (mask word w, bit = its bit).
-__device__ __forceinline__ float2 overflow_sum(const float2* __restrict__ fb, const int* __restrict__ ovf, int i,
-                                               unsigned w, unsigned bit) {
-    int k = ovf[kMaskWords + (i >> 5)] + __popc(w & (bit - 1u));
-    k = min(k, kOvfCap - 1);
-    const float2* o = fb + 2 * kFStride + 2 * k;
-    return cadd(o[0], o[1]);
-}
-
-// Value of half-spectrum bin i (0 <= i <= L) from its scatter slots.
-__device__ __forceinline__ float2 load_bin(const float2* __restrict__ fb, const int* __restrict__ ovf, int i) {
-    float2 v = cadd(fb[i], fb[kFStride + i]);
-    const unsigned w = (unsigned)ovf[i >> 5];
-    const unsigned bit = 1u << (i & 31);
-    if (w & bit) v = cadd(v, overflow_sum(fb, ovf, i, w, bit));
-    return v;
+// F layout per batch row: bins 0..FSTRIDE-1 with two dense slots each
+// (float4 {slot0, slot1} per bin), then 2 x OVF_CAP overflow slots. A bin's
+// value is slot0 + slot1 (+ its two overflow slots if it has more than two
+// contributing taps).
+__device__ __forceinline__ float2 dense_bin(const float2* __restrict__ fb, int i) {
+    const float4 q = reinterpret_cast<const float4*>(fb)[i];
+    return make_float2(q.x + q.z, q.y + q.w);
 }
 
 __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, float2* __restrict__ out,
@@ -92,7 +84,7 @@ __device__ __forceinline__ int inv_col(int w, int c) {
 __global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, float2* __restrict__ out,
                                                  const float2* __restrict__ twp,
                                                  const float2* __restrict__ twn,
-                                                 const int* __restrict__ ovf,
+                                                 const int* __restrict__ fold,
                                                  const float2* __restrict__ tws) {
     using P = Plan<128>;
     __shared__ float2 lds[kColsPerWg * P::US + 1];  // staged bins, then FFT exchange
@@ -103,28 +95,32 @@ __global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, f
     const int col = inv_col(w, c);
     const float2* fb = f + (long)b * kFRow;
     float2* raw = lds + c * P::US;
-    {
-        // both dense planes and the overflow mask word of all 16 bins in one
-        // batch of loads; the rare overflow slots are added afterwards
-        float2 p0[16], p1[16];
-        unsigned mw[16];
+    // fold list entry of this thread: bin | overflow index << 16, or -1
+    const int ent = fold[w * kFoldPerWg + threadIdx.x];
+    float4 q[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 256 * (t + 8 * r) + col;
-            p0[r] = fb[i];
-            p1[r] = fb[kFStride + i];
-            mw[r] = (unsigned)ovf[i >> 5];
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 256 * (t + 8 * r) + col;
-            float2 val = cadd(p0[r], p1[r]);
-            const unsigned bit = 1u << (i & 31);
-            if (mw[r] & bit) val = cadd(val, overflow_sum(fb, ovf, i, mw[r], bit));
-            raw[t + 8 * r] = val;
+    for (int r = 0; r < 16; ++r) q[r] = reinterpret_cast<const float4*>(fb)[256 * (t + 8 * r) + col];
+    float2 oadd = make_float2(0.0f, 0.0f);
+    int opos = -1;
+    if (ent >= 0) {
+        const int bin = ent & 0xffff;
+        const int k = min(ent >> 16, kOvfCap - 1);
+        const float2* o = fb + 2 * kFStride + 2 * k;
+        oadd = cadd(o[0], o[1]);
+        if (bin >= kL) {
+            opos = kColsPerWg * P::US;
+        } else {
+            const int cl = bin & 255, n1 = bin >> 8;
+            const int pp = cl <= 128 ? (cl == 128 ? 0 : cl) : 256 - cl;
+            const int cc = (cl < 128 ? 0 : 8) + (pp & 7);
+            opos = cc * P::US + n1;
         }
     }
-    if (threadIdx.x == 0) lds[kColsPerWg * P::US] = load_bin(fb, ovf, kL);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) raw[t + 8 * r] = make_float2(q[r].x + q[r].z, q[r].y + q[r].w);
+    if (threadIdx.x == 0) lds[kColsPerWg * P::US] = dense_bin(fb, kL);
+    __syncthreads();
+    if (opos >= 0) lds[opos] = cadd(lds[opos], oadd);   // each listed bin appears once
     __syncthreads();
     const float2* mraw = lds + (c ^ 8) * P::US;  // mirror column's bins
     float2 v[16];

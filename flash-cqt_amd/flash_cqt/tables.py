@@ -20,15 +20,15 @@ Everything the kernels need that does not depend on the batch:
            rfft is (N/2) irfft with bins 0 and L doubled, of a conj tap the
            conjugate, of the band's 1/M inverse DFT the forward DFT / M.
            Scatter without atomics: the live taps of one bin (at most 4) are
-           ranked; rank 0 and 1 own dense planes P0[bin], P1[bin], ranks 2-3
-           own two slots of a compact overflow area indexed by the bin's
-           position among the bins of degree > 2. Every (slot, bin) has one
+           ranked; ranks 0 and 1 own the bin's two dense slots (F[2 bin + r]),
+           ranks 2-3 own two slots of a compact overflow area indexed by the
+           bin's position among the bins of degree > 2. Every slot has one
            writer, the set of written slots is fixed by the table, and slots
            never written stay zero, so F needs zeroing only once.
-  ovf_*    per scatter table, int32 [2 * MASK_WORDS]: bit b of word w marks
-           bin 32 w + b as having overflow slots; the second half holds the
-           number of overflow bins before word w (the overflow index of a
-           bin is that prefix plus the popcount of the lower bits).
+  ovf_*    per scatter table, int32 [16][128] fold lists for the inverse
+           column pass: workgroup w (columns 8w..8w+7 and their mirrors) adds
+           the overflow slots of the bins of degree > 2 in its columns;
+           entry = bin | overflow index << 16, -1 = none.
   tasks    band tasks {M, first coefficient, band count, first band}:
            consecutive bands of one group, at most POINTS / M per task.
   tw_pass  W_L^(k1 n2) at k1*256 + n2 (column pass of the packed FFT).
@@ -47,7 +47,7 @@ L = N // 2
 FSTRIDE = L + 64            # complex elements per half-spectrum plane (>= L + 1)
 OVF_CAP = 1024              # bins with more than two contributing taps, per table
 FROW = 2 * FSTRIDE + 2 * OVF_CAP   # complex elements per batch row of F
-MASK_WORDS = (L + 1 + 31) // 32
+FOLD_PER_WG = 128           # fold-list entries per inverse column workgroup (16 per slice)
 XSTRIDE = L + 64            # complex elements per row of the real-FFT spectrum X
 POINTS_PER_TASK = 2048      # 128 threads x 16 values per band workgroup
 STAGE_ORDER = ((16, 2), (16, 4), (16, 8), (16, 16), (256, 2), (256, 4), (256, 8))
@@ -171,11 +171,12 @@ def build(groups, nn=N):
 
 
 def scatter_table(bins, gr, gi):
-    """Slot-assigned scatter records {target | mode << 30, gr} and the overflow map
-    (mode 0: gi = gr, 1: gi = -gr, 2: gi = 0; gr = 0 marks a tap without slot).
+    """Slot-assigned scatter records {target | mode << 30, gr} and the fold
+    lists (mode 0: gi = gr, 1: gi = -gr, 2: gi = 0; gr = 0 marks a tap
+    without slot).
 
     Live taps (gr or gi nonzero) are ranked per bin in coefficient order;
-    target = rank * FSTRIDE + bin for ranks 0-1, and
+    target = 2 bin + rank for ranks 0-1, and
     2 FSTRIDE + 2 * overflow_index(bin) + rank - 2 for ranks 2-3."""
     bins = np.asarray(bins, dtype=np.int64)
     n = bins.size
@@ -195,7 +196,7 @@ def scatter_table(bins, gr, gi):
     oidx = np.full(L + 1, -1, dtype=np.int64)
     oidx[obins] = np.arange(obins.size)
     target = np.zeros(n, dtype=np.int64)
-    tl = np.where(rank < 2, rank * FSTRIDE + sb, 2 * FSTRIDE + 2 * oidx[sb] + (rank - 2))
+    tl = np.where(rank < 2, 2 * sb + rank, 2 * FSTRIDE + 2 * oidx[sb] + (rank - 2))
     target[order] = tl
     assert target.max() < FROW
     gr = np.where(live, gr, 0.0)
@@ -206,13 +207,29 @@ def scatter_table(bins, gr, gi):
     rec = np.zeros((n, 2), dtype=np.int32)
     rec[:, 0] = target | (mode << 30)
     rec[:, 1] = _bits(gr)
-    mask = np.zeros(MASK_WORDS * 32, dtype=np.uint64)
-    mask[obins] = 1
-    words = (mask.reshape(MASK_WORDS, 32) << np.arange(32, dtype=np.uint64)).sum(1)
-    counts = mask.reshape(MASK_WORDS, 32).sum(1).astype(np.int64)
-    prefix = np.concatenate(([0], np.cumsum(counts)[:-1]))
-    ovf = np.concatenate([words.astype(np.uint32).view(np.int32), prefix.astype(np.int32)])
+    ovf = fold_lists(obins)
     return rec, ovf
+
+
+def inverse_column_wg(col):
+    """Workgroup of the inverse column pass that owns column col (0..255):
+    workgroup w holds columns 8w..8w+7 and their mirrors 256 - p; pair 0
+    is {0, 128}."""
+    p = col if col < 128 else (0 if col == 128 else 256 - col)
+    return p // 8
+
+
+def fold_lists(obins):
+    """Per inverse-column workgroup list of (bin | overflow index << 16)."""
+    lists = [[] for _ in range(16)]
+    for k, b in enumerate(np.asarray(obins).tolist()):
+        w = 0 if b == L else inverse_column_wg(b & 255)
+        lists[w].append(b | (k << 16))
+    out = np.full((16, FOLD_PER_WG), -1, dtype=np.int64)
+    for w, lst in enumerate(lists):
+        assert len(lst) <= FOLD_PER_WG, "fold list overflow"
+        out[w, :len(lst)] = lst
+    return out.astype(np.int32).reshape(-1)
 
 
 def check_tasks(tasks, ncoef, bands, points=POINTS_PER_TASK):

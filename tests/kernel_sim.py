@@ -227,16 +227,24 @@ def _row_pass(Y, inverse):
     return out
 
 
-def load_bins(Fs, ovf, i):
-    """Value of bins i from the slot buffer Fs [FROW] (packed_fft.hip load_bin)."""
-    v = Fs[i] + Fs[T.FSTRIDE + i]
-    w = ovf[i >> 5].view(np.uint32).astype(np.int64)
-    bit = (w >> (i & 31)) & 1
-    k = ovf[T.MASK_WORDS + (i >> 5)] + np.array([bin(int(x) & ((1 << int(b)) - 1)).count("1")
-                                                 for x, b in zip(w.reshape(-1), (i & 31).reshape(-1))]).reshape(i.shape)
-    k = np.minimum(k, T.OVF_CAP - 1)
-    o = 2 * T.FSTRIDE + 2 * k
-    return np.where(bit == 1, v + Fs[o] + Fs[o + 1], v)
+def staged_bins(Fs, fold):
+    """Bin values [L+1] as k_col_inv stages them: dense slots 2 bin, 2 bin + 1,
+    plus the two overflow slots of every bin on a workgroup's fold list
+    (each listed bin once, owned by the workgroup of its column)."""
+    dense = Fs[0:2 * (L + 1):2] + Fs[1:2 * (L + 1):2]
+    out = dense.copy()
+    seen = set()
+    for w in range(16):
+        for ent in fold[w * T.FOLD_PER_WG:(w + 1) * T.FOLD_PER_WG].tolist():
+            if ent < 0:
+                continue
+            b, k = ent & 0xFFFF, min(ent >> 16, T.OVF_CAP - 1)
+            assert b not in seen
+            seen.add(b)
+            assert b == L or T.inverse_column_wg(b & 255) == w
+            o = 2 * T.FSTRIDE + 2 * k
+            out[b] += Fs[o] + Fs[o + 1]
+    return out
 
 
 def inv_col(w, c):
@@ -246,7 +254,8 @@ def inv_col(w, c):
 
 def packed_fft_inv(F, ovf=None):
     """k_col_inv (paired columns, retangle from staged bins) + k_row_inv.
-    F is a plain half spectrum [B, L+1] or, with ovf, the slot buffer [B, FROW]."""
+    F is a plain half spectrum [B, L+1] or, with the fold lists, the slot
+    buffer [B, FROW]."""
     F = np.asarray(F, dtype=np.complex128)
     B = F.shape[0]
     twn = _c(T.half_twiddles())
@@ -255,7 +264,8 @@ def packed_fft_inv(F, ovf=None):
     tt = np.arange(8)
     n1s = np.arange(128)
     for b in range(B):
-        get = (lambda i: F[b][i]) if ovf is None else (lambda i: load_bins(F[b], ovf, i))
+        Fb = F[b] if ovf is None else staged_bins(F[b], ovf)
+        get = lambda i: Fb[i]
         nyq = get(np.array([L]))[0]
         for w in range(16):
             cols = np.array([inv_col(w, c) for c in range(16)])

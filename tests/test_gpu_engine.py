@@ -88,16 +88,16 @@ def test_packed_fft_matches_numpy(fused, B):
 
 @pytest.mark.parametrize("B", [1, 2])
 def test_inverse_tail_matches_irfft(fused, B):
-    """Half spectrum split over the two dense slot planes (overflow slots zero)."""
+    """Half spectrum split over each bin's two dense slots (overflow slots zero)."""
     from flash_cqt import tables as T
     rs = np.random.RandomState(200 + B)
     F = (rs.standard_normal((B, L + 1)) + 1j * rs.standard_normal((B, L + 1))).astype(np.complex64)
     a = (rs.uniform(size=(B, L + 1))).astype(np.float32)
     f = torch.zeros(B, T.FROW, 2, device=_dev())
-    f[:, :L + 1, 0] = gpu(F.real * a)
-    f[:, :L + 1, 1] = gpu(F.imag * a)
-    f[:, T.FSTRIDE:T.FSTRIDE + L + 1, 0] = gpu(F.real * (1 - a))
-    f[:, T.FSTRIDE:T.FSTRIDE + L + 1, 1] = gpu(F.imag * (1 - a))
+    f[:, 0:2 * (L + 1):2, 0] = gpu(F.real * a)
+    f[:, 0:2 * (L + 1):2, 1] = gpu(F.imag * a)
+    f[:, 1:2 * (L + 1):2, 0] = gpu(F.real * (1 - a))
+    f[:, 1:2 * (L + 1):2, 1] = gpu(F.imag * (1 - a))
     y = torch.empty(B, N, device=_dev())
     w = fused._workspace(B)
     fused.packed_ifft(f, y, w["W"])

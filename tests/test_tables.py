@@ -98,20 +98,23 @@ def test_inverse_tail_drops_edge_imaginary_parts():
     assert snr_db(np.fft.irfft(F, n=N), y) > 140
 
 
-def test_scatter_slots_unique_and_overflow_map(factored_tables):
-    """Every live tap owns one slot; overflow bins match the map; a bin's
-    slots are exactly its live taps."""
+def test_scatter_slots_unique_and_fold_lists(factored_tables):
+    """Every live tap owns one slot; the fold lists name every bin with
+    overflow slots exactly once, in the workgroup that owns its column."""
     from flash_cqt import tables as T
     for name in ("scat", "scat_a"):
         rec = factored_tables[name]
-        ovf = factored_tables["ovf_" + name]
+        fold = factored_tables["ovf_" + name]
         live = rec[:, 1] != 0
         tgt = (rec[live, 0].view(np.uint32) & 0x3FFFFFFF).astype(np.int64)
         assert np.unique(tgt).size == tgt.size
         assert tgt.max() < T.FROW
-        words = ovf[:T.MASK_WORDS].view(np.uint32)
-        flagged = np.flatnonzero(((words[:, None] >> np.arange(32, dtype=np.uint32)) & 1).reshape(-1))
-        n_over = int((tgt >= 2 * T.FSTRIDE).sum())
-        assert n_over >= flagged.size and flagged.size <= T.OVF_CAP
-        prefix = ovf[T.MASK_WORDS:]
-        assert prefix[0] == 0 and (np.diff(prefix) >= 0).all()
+        over = tgt[tgt >= 2 * T.FSTRIDE]
+        ks = np.unique((over - 2 * T.FSTRIDE) // 2)
+        ents = fold[fold >= 0]
+        assert np.array_equal(np.sort(ents >> 16), ks)
+        assert np.unique(ents & 0xFFFF).size == ents.size
+        for w in range(16):
+            for e in fold[w * T.FOLD_PER_WG:(w + 1) * T.FOLD_PER_WG]:
+                if e >= 0 and (e & 0xFFFF) != T.L:
+                    assert T.inverse_column_wg(int(e) & 255) == w
