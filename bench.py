@@ -211,6 +211,27 @@ def kernel_timings(f, B, reps):
     return out
 
 
+KERNEL_SYMBOL = {"packed_fft": ("k_col_fwd", "k_row_fwd"), "route_bands": ("k_route_bands<0>",),
+                 "scatter_bands": ("k_scatter_bands<0>",), "packed_ifft": ("k_col_inv", "k_row_inv")}
+
+
+def measured_traffic(name, B):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, copy-calibrated), or None."""
+    path = ROOT / "profiles" / "hbm_traffic_b64.txt"
+    if B != 64 or not path.exists():
+        return None
+    got = {}
+    for ln in path.read_text().splitlines():
+        if ln.startswith("TRAFFIC "):
+            parts = ln.split()
+            got[parts[1]] = float(parts[3].split("=")[1])
+    syms = KERNEL_SYMBOL[name]
+    if not all(s in got for s in syms):
+        return None
+    return sum(got[s] for s in syms) / len(syms)
+
+
 def kernels_only(f, B, reps):
     """A few launches of each kernel and one plain copy of known size, for
     rocprofv3 --pmc runs (FETCH_SIZE / WRITE_SIZE calibration)."""
@@ -323,8 +344,11 @@ def main():
     single = {k: v for k, v in kern.items() if v["launches"] == 1}
     dom = max(single, key=lambda k: single[k]["ms_per_launch"])
     ach = kern[dom]["gbps"]
+    traffic = measured_traffic(dom, B)
     roof = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": PEAK_GBPS, "unit": "GB/s",
-            "frac": ach / PEAK_GBPS, "traffic": None,
+            "frac": ach / PEAK_GBPS, "traffic": traffic,
+            "traffic_source": "profiles/hbm_traffic_b64.txt (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0)"
+            if traffic else None,
             "alg_bytes_per_launch": kern[dom]["alg_bytes_per_call"],
             "ms_per_launch": kern[dom]["ms_per_launch"], "batch": B}
 
