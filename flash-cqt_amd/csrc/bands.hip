@@ -63,22 +63,36 @@ __device__ __forceinline__ void route_band(const int4 task, const int b, const f
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
     const long cb = (long)task.y + (long)u * M;
-    const int4 bd = bands[task.w + (active ? u : 0)];   // {centre bin, r, l, 0}
+    const int4 bd = bands[task.w + (active ? u : 0)];   // {centre bin, r, l, side flag}
     const float2* xb = xs + (long)b * kXStride;
     // indices first, then every load at once (branch-free, clamped in bounds),
     // so the 32 loads of a thread are in flight together
+    // tap j < r reads bin c + j, tap j >= M - l reads bin c + j - M; octave
+    // bands never leave (0, N/2) (checked when the tables are built), the DC
+    // and Nyquist side bands (flag bd.w) wrap mod N and fold past N/2 with
+    // conjugation. Dead taps read bin c and are zeroed.
     int kk[16];
     unsigned live = 0, cj = 0;
+    if (bd.w == 0) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int j = t + P::T * r;
-        int k = bd.x + (j < bd.y ? j : j - M);
-        k += k < 0 ? kN : 0;
-        const bool c = k > kL;
-        k = c ? kN - k : k;
-        kk[r] = min(max(k, 0), kL);
-        live |= (active && (j < bd.y || j >= M - bd.z)) ? 1u << r : 0u;
-        cj |= c ? 1u << r : 0u;
+        for (int r = 0; r < 16; ++r) {
+            const int j = t + P::T * r;
+            const bool lv = active && (j < bd.y || j >= M - bd.z);
+            kk[r] = lv ? bd.x + j - (j < bd.y ? 0 : M) : bd.x;
+            live |= lv ? 1u << r : 0u;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int j = t + P::T * r;
+            int k = bd.x + (j < bd.y ? j : j - M);
+            k += k < 0 ? kN : 0;
+            const bool c = k > kL;
+            k = c ? kN - k : k;
+            kk[r] = min(max(k, 0), kL);
+            live |= (active && (j < bd.y || j >= M - bd.z)) ? 1u << r : 0u;
+            cj |= c ? 1u << r : 0u;
+        }
     }
     const long wb = active ? cb : (long)task.y;
     float w[16];

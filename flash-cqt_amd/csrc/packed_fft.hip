@@ -87,7 +87,7 @@ __global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, f
                                                  const int* __restrict__ fold,
                                                  const float2* __restrict__ tws) {
     using P = Plan<128>;
-    __shared__ float2 lds[kColsPerWg * P::US + 1];  // staged bins, then FFT exchange
+    __shared__ float2 lds[kColsPerWg * P::US];  // staged bins, then FFT exchange
     const int b = blockIdx.x / kColWgs;
     const int w = blockIdx.x - b * kColWgs;
     const int c = threadIdx.x & (kColsPerWg - 1);
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, f
         const float2* o = fb + 2 * kFStride + 2 * k;
         oadd = cadd(o[0], o[1]);
         if (bin >= kL) {
-            opos = kColsPerWg * P::US;
+            opos = 128;                          // column 0's pad slot holds bin L
         } else {
             const int cl = bin & 255, n1 = bin >> 8;
             const int pp = cl <= 128 ? (cl == 128 ? 0 : cl) : 256 - cl;
@@ -118,29 +118,34 @@ __global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, f
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) raw[t + 8 * r] = make_float2(q[r].x + q[r].z, q[r].y + q[r].w);
-    if (threadIdx.x == 0) lds[kColsPerWg * P::US] = dense_bin(fb, kL);
+    // bin L is parked in column 0's pad slot raw[128] (column 0 is slot 0 of
+    // workgroup 0)
+    if (col == 0 && t == 0) raw[128] = dense_bin(fb, kL);
     __syncthreads();
     if (opos >= 0) lds[opos] = cadd(lds[opos], oadd);   // each listed bin appears once
     __syncthreads();
-    const float2* mraw = lds + (c ^ 8) * P::US;  // mirror column's bins
+    if (col == 0 && t == 0) {          // bins 0 and L are real for irfft (after any fold)
+        raw[0].y = 0.0f;
+        raw[128].y = 0.0f;
+    }
+    __syncthreads();
+    // mirror bin L - i: column 256 - col at row 127 - n1; columns 0 and 128
+    // are their own mirrors (column 0 at row 128 - n1, row 128 = bin L)
+    const float2* mp = (col == 0 || col == 128) ? raw : lds + (c ^ 8) * P::US;
+    const int moff = col == 0 ? 128 : 127;
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int n1 = t + 8 * r;
         const int i = 256 * n1 + col;
-        float2 f0 = raw[n1];
-        float2 f1;
-        if (col == 0) f1 = n1 == 0 ? lds[kColsPerWg * P::US] : raw[128 - n1];
-        else if (col == 128) f1 = raw[127 - n1];
-        else f1 = mraw[127 - n1];
-        if (i == 0) {  // bins 0 and L are real for irfft
-            f0.y = 0.0f;
-            f1.y = 0.0f;
-        }
-        const float2 e = make_float2(0.5f * (f0.x + f1.x), 0.5f * (f0.y - f1.y));
-        const float2 d = make_float2(0.5f * (f0.x - f1.x), 0.5f * (f0.y + f1.y));
+        const float2 f0 = raw[n1];
+        const float2 f1 = mp[moff - n1];
+        // 2W = conj(S + i D conj(W_N^i)) with S = f0 + conj f1, D = f0 - conj f1;
+        // the factor 2 is removed by the 1/(2L) of the unpack
+        const float2 sm = make_float2(f0.x + f1.x, f0.y - f1.y);
+        const float2 d = make_float2(f0.x - f1.x, f0.y + f1.y);
         const float2 o = cmulc(d, twn[i]);
-        v[r] = make_float2(e.x - o.y, -(e.y + o.x));
+        v[r] = make_float2(sm.x - o.y, -(sm.y + o.x));
     }
     __syncthreads();  // staged bins fully consumed before the FFT reuses LDS
     fft_unit<128, -1>(v, lds + c * P::US, t, tws);
@@ -201,21 +206,21 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
     row_fft_to_lds(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, rho, t, tws);
     // untangle: lanes walk the tile's rows for coalesced stores
     const float2* s = lds + rho2 * P::US;
-    const float2* sm = lds + (rho2 ^ 8) * P::US;   // mirror row (rows 0 / 64: own row)
+    // mirror bin L - k: row 128 - k1 at column 255 - k2; rows 0 and 64 are
+    // their own mirrors (row 0 at column (256 - k2) mod 256)
+    const float2* mp = (k1 == 0 || k1 == 64) ? s : lds + (rho2 ^ 8) * P::US;
+    const int mcol = k1 == 0 ? 256 : 255;
     float2* xb = xs + (long)b * kXStride;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const int k2 = kg + 16 * u;
-        const int k = k1 + 128 * k2;
         const float2 z = s[pad16(k2)];
-        float2 zm;
-        if (k1 == 0) zm = s[pad16((256 - k2) & 255)];
-        else if (k1 == 64) zm = s[pad16(255 - k2)];
-        else zm = sm[pad16(255 - k2)];
-        // W = W_N^k; cA = (1 + Im W, -Re W)/2, cB = (1 - Im W, Re W)/2, X = cA z + cB conj(zm)
-        const float2 ca = make_float2(0.5f * (1.0f + wn[u].y), -0.5f * wn[u].x);
-        const float2 cb = make_float2(0.5f * (1.0f - wn[u].y), 0.5f * wn[u].x);
-        xb[k] = cadd(cmul(ca, z), cmulc(cb, zm));
+        const float2 zm = mp[pad16((mcol - k2) & 255)];
+        // X = E + W O,  E = (z + conj zm)/2,  O = (z - conj zm)/(2i),  W = W_N^k
+        const float2 sm = make_float2(z.x + zm.x, z.y - zm.y);
+        const float2 d = make_float2(z.x - zm.x, z.y + zm.y);
+        xb[k1 + 128 * k2] = make_float2(0.5f * fmaf(wn[u].x, d.y, fmaf(wn[u].y, d.x, sm.x)),
+                                        0.5f * fmaf(wn[u].y, d.y, fmaf(-wn[u].x, d.x, sm.y)));
     }
     if (w == 0 && threadIdx.x == 0) {               // Nyquist bin from Z[0] (row 0, k2 = 0)
         const float2 z0 = lds[pad16(0)];
@@ -236,7 +241,7 @@ __global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, 
     const int kg = threadIdx.x >> 4;
     const float2* s2 = lds + rho2 * P::US;
     const int kk1 = rg * kRowsPerWg + rho2;
-    constexpr float sc = 1.0f / (float)kL;
+    constexpr float sc = 0.5f / (float)kL;     // 1/L of the inverse, 1/2 of the retangle
     float2* yo = y + (long)b * kL;  // y viewed as [batch][32768] float pairs
 #pragma unroll
     for (int u = 0; u < 16; ++u) {

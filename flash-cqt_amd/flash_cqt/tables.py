@@ -10,9 +10,11 @@ Everything the kernels need that does not depend on the batch:
            (2/N)(1 - [k in {0, L}]/2) (the transpose of irfft is (2/N) rfft
            with bins 0 and L halved; the band's transpose of the forward DFT
            is the unscaled inverse DFT).
-  bands    per band {centre bin c, r, l, 0}: tap j < r reads bin c + j, tap
-           j >= M - l reads bin c + j - M (mod N; bins past N/2 fold to N - k
-           with conjugation), the taps between lie outside the window.
+  bands    per band {centre bin c, r, l, side}: tap j < r reads bin c + j,
+           tap j >= M - l reads bin c + j - M (mod N; bins past N/2 fold to
+           N - k with conjugation), the taps between lie outside the window.
+           side = 1 marks the bands whose taps reach bin 0 or N/2 or beyond
+           (DC, Nyquist); the others take the kernel's no-wrap path.
   scat     synthesis record per tap, 2 x int32 {slot | mode << 30, gain}:
            the half spectrum is F[pos] = sum over taps of gdv DFT(C).
   scat_a   analysis-adjoint record {slot of idx | mode << 30, gr} with
@@ -120,7 +122,10 @@ def band_descriptors(groups, nn=N):
             r = int(lo.max()) + 1 if lo.size else 0
             l = int(M - hi.min()) if hi.size else 0
             c = int(unwrapped[i, 0])
-            rows.append([c, r, l, 0])
+            # side flag: taps may wrap mod nn or fold past nn/2 (DC, Nyquist)
+            k = c + np.concatenate([np.arange(r), np.arange(M - l, M) - M])
+            side = int(bool(np.any(k <= 0) or np.any(k >= nn // 2)))
+            rows.append([c, r, l, side])
     return np.asarray(rows, dtype=np.int32)
 
 
