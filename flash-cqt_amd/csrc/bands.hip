@@ -38,13 +38,13 @@ constexpr int kBandLds = cmax(cmax(cmax(band_lds(32), band_lds(64)), cmax(band_l
                               cmax(cmax(band_lds(512), band_lds(1024)), band_lds(2048)));
 
 template <int LAYOUT>
-__device__ __forceinline__ float2 load_coef(const float* __restrict__ cre, const float* __restrict__ cim, long i) {
+__device__ __forceinline__ float2 load_coef(const float* __restrict__ cre, const float* __restrict__ cim, int i) {
     if constexpr (LAYOUT == FCQT_PLANAR) return make_float2(cre[i], cim[i]);
     else return reinterpret_cast<const float2*>(cre)[i];
 }
 
 template <int LAYOUT>
-__device__ __forceinline__ void store_coef(float* __restrict__ cre, float* __restrict__ cim, long i, float2 v) {
+__device__ __forceinline__ void store_coef(float* __restrict__ cre, float* __restrict__ cim, int i, float2 v) {
     if constexpr (LAYOUT == FCQT_PLANAR) {
         cre[i] = v.x;
         cim[i] = v.y;
@@ -62,61 +62,65 @@ __device__ __forceinline__ void route_band(const int4 task, const int b, const f
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
-    const long cb = (long)task.y + (long)u * M;
     const int4 bd = bands[task.w + (active ? u : 0)];   // {centre bin, r, l, side flag}
-    const float2* xb = xs + (long)b * kXStride;
-    // indices first, then every load at once (branch-free, clamped in bounds),
-    // so the 32 loads of a thread are in flight together
-    // tap j < r reads bin c + j, tap j >= M - l reads bin c + j - M; octave
-    // bands never leave (0, N/2) (checked when the tables are built), the DC
-    // and Nyquist side bands (flag bd.w) wrap mod N and fold past N/2 with
-    // conjugation. Dead taps read bin c and are zeroed.
-    int kk[16];
-    unsigned live = 0, cj = 0;
-    if (bd.w == 0) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int j = t + P::T * r;
-            const bool lv = active && (j < bd.y || j >= M - bd.z);
-            kk[r] = lv ? bd.x + j - (j < bd.y ? 0 : M) : bd.x;
-            live |= lv ? 1u << r : 0u;
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int j = t + P::T * r;
-            int k = bd.x + (j < bd.y ? j : j - M);
-            k += k < 0 ? kN : 0;
-            const bool c = k > kL;
-            k = c ? kN - k : k;
-            kk[r] = min(max(k, 0), kL);
-            live |= (active && (j < bd.y || j >= M - bd.z)) ? 1u << r : 0u;
-            cj |= c ? 1u << r : 0u;
-        }
-    }
-    const long wb = active ? cb : (long)task.y;
-    float w[16];
-    float2 xv[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        w[r] = wt[wb + t + P::T * r];
-        xv[r] = xb[kk[r]];
-    }
+    const float2* xb = xs + (long)b * kXStride;             // uniform bases, 32-bit offsets
+    const float* wu = wt + task.y;
+    const int ub = active ? u * M : 0;
+    // tap j < r reads bin c + j, tap j >= M - l reads bin c + j - M. Weights
+    // are exactly zero outside the window, so a dead tap only needs an
+    // in-bounds bin; units past the task's band count compute garbage that
+    // is never stored. Octave bands never leave (0, N/2) (checked when the
+    // tables are built); the DC and Nyquist side bands (flag bd.w) fold
+    // bins below 0 or above N/2 back with conjugation.
     float2 v[16];
+    if (bd.w == 0) {
+        int kk[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const float ww = (live >> r) & 1u ? w[r] : 0.0f;
-        v[r] = make_float2(ww * xv[r].x, (cj >> r) & 1u ? -ww * xv[r].y : ww * xv[r].y);
+        for (int r = 0; r < 16; ++r) {
+            const int j = t + P::T * r;
+            kk[r] = min(max(bd.x + j - (j < bd.y ? 0 : M), 0), kL);
+        }
+        float w[16];
+        float2 xv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            w[r] = wu[ub + t + P::T * r];
+            xv[r] = xb[kk[r]];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = make_float2(w[r] * xv[r].x, w[r] * xv[r].y);
+    } else {
+        int kk[16];
+        unsigned cj = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int j = t + P::T * r;
+            const int kp = bd.x + j - (j < bd.y ? 0 : M);
+            const bool neg = kp < 0, over = kp > kL;
+            kk[r] = min(max(neg ? -kp : (over ? kN - kp : kp), 0), kL);
+            cj |= (neg || over) ? 1u << r : 0u;
+        }
+        float w[16];
+        float2 xv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            w[r] = wu[ub + t + P::T * r];
+            xv[r] = xb[kk[r]];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            v[r] = make_float2(w[r] * xv[r].x, (cj >> r) & 1u ? -w[r] * xv[r].y : w[r] * xv[r].y);
     }
     fft_unit<M, +1>(v, lds + u * P::US, t, tws);
     if (active) {
-        const long ob = (long)b * ncoef + cb;
+        const long ob = (long)b * ncoef + task.y;           // uniform
 #pragma unroll
         for (int q = 0; q < P::QL; ++q) {
 #pragma unroll
             for (int r = 0; r < P::RL; ++r) {
-                const int m = t + P::T * q + r * P::OS;
-                store_coef<LAYOUT>(cre, cim, ob + m, v[q * P::RL + r]);
+                const int m = ub + t + P::T * q + r * P::OS;
+                store_coef<LAYOUT>(cre + (LAYOUT == FCQT_PLANAR ? ob : 2 * ob),
+                                   cim + (LAYOUT == FCQT_PLANAR ? ob : 0), m, v[q * P::RL + r]);
             }
         }
     }
@@ -131,21 +135,22 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
-    const long cb = (long)task.y + (long)u * M;
-    const long ib = (long)b * ncoef + cb;
+    const int ub = active ? u * M : 0;
+    const long ib = (long)b * ncoef + task.y;               // uniform
+    const float* cr = cre + (LAYOUT == FCQT_PLANAR ? ib : 2 * ib);
+    const float* ci = cim + (LAYOUT == FCQT_PLANAR ? ib : 0);
     float2 v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-        v[r] = active ? load_coef<LAYOUT>(cre, cim, ib + t + P::T * r) : make_float2(0.0f, 0.0f);
+    for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, ub + t + P::T * r);
     fft_unit<M, -1>(v, lds + u * P::US, t, tws);
     // records {slot | mode << 30, gain}: mode 0 gi = gr, 1 gi = -gr, 2 gi = 0;
     // gain 0 = no slot. All 16 loads issue before the first store.
-    const long rb = active ? cb : (long)task.y;
+    const int2* st = scat + task.y;                        // uniform
     int2 rec[16];
 #pragma unroll
     for (int q = 0; q < P::QL; ++q)
 #pragma unroll
-        for (int r = 0; r < P::RL; ++r) rec[q * P::RL + r] = scat[rb + t + P::T * q + r * P::OS];
+        for (int r = 0; r < P::RL; ++r) rec[q * P::RL + r] = st[ub + t + P::T * q + r * P::OS];
     if (active) {
         float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
 #pragma unroll

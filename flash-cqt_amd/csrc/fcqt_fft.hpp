@@ -201,18 +201,24 @@ struct Plan {
 
 // One Stockham stage read: butterflies j = t + T q, inputs j + r M/R,
 // twiddle W_{NS R}^{r (j mod NS)}, radix-R DFT, results into v[q R + r].
+// M/R is a multiple of 16 in every stage that reads LDS, so
+// pad16(j + r M/R) = pad16(j) + r (M/R)(17/16): one address per butterfly,
+// constant offsets for r (immediate offsets of the LDS instructions).
 template <int M, int R, int NS, int SIGN>
 __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
                                            const float2* __restrict__ tws) {
     constexpr int T = M / 16;
     constexpr int Q = 16 / R;
     constexpr int STRIDE = M / R;
+    static_assert(STRIDE % 16 == 0, "padded stride");
+    constexpr int PSTRIDE = STRIDE + STRIDE / 16;
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int j = t + T * q;
+        const float2* sj = s + pad16(j);
         float2 a[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) a[r] = s[pad16(j + r * STRIDE)];
+        for (int r = 0; r < R; ++r) a[r] = sj[r * PSTRIDE];
         if constexpr (NS > 1) {
             const int k = j & (NS - 1);
             float2 w[R];
@@ -227,17 +233,21 @@ __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
 }
 
 // Stockham stage write: butterfly j's result r goes to
-// (j / NS) NS R + (j mod NS) + r NS.
+// (j / NS) NS R + (j mod NS) + r NS. NS is 1 (R = 16: 16 consecutive slots,
+// one pad slot after them) or 16 (pad16(base + 16 r) = pad16(base) + 17 r).
 template <int M, int R, int NS>
 __device__ __forceinline__ void stage_write(const float2* v, float2* s, int t) {
     constexpr int T = M / 16;
     constexpr int Q = 16 / R;
+    static_assert((NS == 1 && R == 16) || NS == 16, "stage write layout");
+    constexpr int PS = NS == 1 ? 1 : 17;
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int j = t + T * q;
         const int base = (j / NS) * NS * R + (j & (NS - 1));
+        float2* sb = s + pad16(base);
 #pragma unroll
-        for (int r = 0; r < R; ++r) s[pad16(base + r * NS)] = v[q * R + r];
+        for (int r = 0; r < R; ++r) sb[r * PS] = v[q * R + r];
     }
 }
 

@@ -260,13 +260,19 @@ def tap_bins(c, r, l, M, nn=N):
 
 
 def check_band_taps(bands, groups, nn=N):
-    """The descriptor rule must reproduce the gather table on every live tap."""
+    """The descriptor rule must reproduce the gather table on every live tap,
+    and both weight rows (window and dual window) must be exactly zero on
+    the dead taps r <= j < M - l: the band kernels gather a clamped bin there
+    and rely on the zero weight instead of a select."""
     bi = 0
     for idx, gv, pos, gdv, conj in groups:
         b, M = idx.shape
         for i in range(b):
             c, r, l, _ = bands[bi].tolist()
             k, cj = tap_bins(c, r, l, M, nn)
+            dead = np.zeros(M, dtype=bool)
+            dead[r:M - l] = True
+            assert not np.any(gv[i][dead]) and not np.any(gdv[i][dead]), "nonzero weight on a dead tap"
             live = gv[i] != 0
             assert np.array_equal(k[live], idx[i][live]), "band descriptor disagrees with the gather table"
             assert np.array_equal(cj[live], conj[i][live])
