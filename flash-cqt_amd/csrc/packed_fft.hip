@@ -13,7 +13,7 @@
 // and it writes the real FFT X[0..L] itself (X[L] = Re Z[0] - Im Z[0]).
 // Inverse: the column pass pairs every column n2 with its mirror 256 - n2
 // (columns 0 and 128 are their own mirrors), stages each bin's value (the sum
-// of its scatter slots: two dense slots plus, for the bins on the table's
+// of its scatter slots: two dense slot planes plus, for the bins on the table's
 // overflow fold list of this workgroup, two overflow slots) in LDS, and
 // retangles there,
 //   E = (F[i] + conj F[L-i])/2,  O = (F[i] - conj F[L-i])/2 conj(W_N^i),
@@ -32,17 +32,19 @@ namespace fcqt {
 constexpr int kColsPerWg = 16;                 // column pass: 16 columns x 128 rows
 constexpr int kRowsPerWg = 16;                 // row pass: 16 rows x 256 columns
 constexpr int kColWgs = 256 / kColsPerWg;      // 16 workgroups per slice
+constexpr int kInvColsPerWg = 32;              // inverse column pass: 16 columns + 16 mirrors
+constexpr int kInvWgs = 256 / kInvColsPerWg;   // 8 workgroups per slice
+constexpr int kInvThreads = 8 * kInvColsPerWg;
 constexpr int kRowWgs = 128 / kRowsPerWg;      // 8 workgroups per slice
 
 // ------------------------------------------------------------ column pass
 
-// F layout per batch row: bins 0..FSTRIDE-1 with two dense slots each
-// (float4 {slot0, slot1} per bin), then 2 x OVF_CAP overflow slots. A bin's
-// value is slot0 + slot1 (+ its two overflow slots if it has more than two
-// contributing taps).
+// F layout per batch row: two dense slot planes of FSTRIDE bins (plane r
+// holds the rank-r tap of each bin), then 2 x OVF_CAP overflow slots. A
+// bin's value is plane0 + plane1 (+ its two overflow slots if it has more
+// than two contributing taps).
 __device__ __forceinline__ float2 dense_bin(const float2* __restrict__ fb, int i) {
-    const float4 q = reinterpret_cast<const float4*>(fb)[i];
-    return make_float2(q.x + q.z, q.y + q.w);
+    return cadd(fb[i], fb[kFStride + i]);
 }
 
 __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, float2* __restrict__ out,
@@ -73,33 +75,37 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
     }
 }
 
-// Column of local slot c in inverse column workgroup w: slots 0-7 hold
-// columns p = 8w..8w+7, slots 8-15 their mirrors 256 - p; pair p = 0 is
-// {0, 128} (both self-mirrored).
+// Column of local slot c in inverse column workgroup w: slots 0-15 hold
+// columns p = 16w..16w+15, slots 16-31 their mirrors 256 - p; pair p = 0 is
+// {0, 128} (both self-mirrored). Each half is 16 consecutive columns, so
+// every row of the tile reads and writes whole 128-byte lines.
 __device__ __forceinline__ int inv_col(int w, int c) {
-    const int p = 8 * w + (c & 7);
-    return c < 8 ? p : (p == 0 ? 128 : 256 - p);
+    const int p = 16 * w + (c & 15);
+    return c < 16 ? p : (p == 0 ? 128 : 256 - p);
 }
 
-__global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, float2* __restrict__ out,
-                                                 const float2* __restrict__ twp,
-                                                 const float2* __restrict__ twn,
-                                                 const int* __restrict__ fold,
-                                                 const float2* __restrict__ tws) {
+__global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restrict__ f, float2* __restrict__ out,
+                                                         const float2* __restrict__ twp,
+                                                         const float2* __restrict__ twn,
+                                                         const int* __restrict__ fold,
+                                                         const float2* __restrict__ tws) {
     using P = Plan<128>;
-    __shared__ float2 lds[kColsPerWg * P::US];  // staged bins, then FFT exchange
-    const int b = blockIdx.x / kColWgs;
-    const int w = blockIdx.x - b * kColWgs;
-    const int c = threadIdx.x & (kColsPerWg - 1);
-    const int t = threadIdx.x >> 4;
+    __shared__ float2 lds[kInvColsPerWg * P::US];  // staged bins, then FFT exchange
+    const int b = blockIdx.x / kInvWgs;
+    const int w = blockIdx.x - b * kInvWgs;
+    const int c = threadIdx.x & (kInvColsPerWg - 1);
+    const int t = threadIdx.x >> 5;
     const int col = inv_col(w, c);
     const float2* fb = f + (long)b * kFRow;
     float2* raw = lds + c * P::US;
     // fold list entry of this thread: bin | overflow index << 16, or -1
     const int ent = fold[w * kFoldPerWg + threadIdx.x];
-    float4 q[16];
+    float2 q0[16], q1[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) q[r] = reinterpret_cast<const float4*>(fb)[256 * (t + 8 * r) + col];
+    for (int r = 0; r < 16; ++r) {
+        q0[r] = fb[256 * (t + 8 * r) + col];
+        q1[r] = fb[kFStride + 256 * (t + 8 * r) + col];
+    }
     float2 oadd = make_float2(0.0f, 0.0f);
     int opos = -1;
     if (ent >= 0) {
@@ -112,12 +118,12 @@ __global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, f
         } else {
             const int cl = bin & 255, n1 = bin >> 8;
             const int pp = cl <= 128 ? (cl == 128 ? 0 : cl) : 256 - cl;
-            const int cc = (cl < 128 ? 0 : 8) + (pp & 7);
+            const int cc = (cl < 128 ? 0 : 16) + (pp & 15);
             opos = cc * P::US + n1;
         }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) raw[t + 8 * r] = make_float2(q[r].x + q[r].z, q[r].y + q[r].w);
+    for (int r = 0; r < 16; ++r) raw[t + 8 * r] = cadd(q0[r], q1[r]);
     // bin L is parked in column 0's pad slot raw[128] (column 0 is slot 0 of
     // workgroup 0)
     if (col == 0 && t == 0) raw[128] = dense_bin(fb, kL);
@@ -131,7 +137,7 @@ __global__ __launch_bounds__(128) void k_col_inv(const float2* __restrict__ f, f
     __syncthreads();
     // mirror bin L - i: column 256 - col at row 127 - n1; columns 0 and 128
     // are their own mirrors (column 0 at row 128 - n1, row 128 = bin L)
-    const float2* mp = (col == 0 || col == 128) ? raw : lds + (c ^ 8) * P::US;
+    const float2* mp = (col == 0 || col == 128) ? raw : lds + (c ^ 16) * P::US;
     const int moff = col == 0 ? 128 : 127;
     float2 v[16];
 #pragma unroll
@@ -281,7 +287,7 @@ extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, c
         !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16) || !aligned(ovf, 4))
         return FCQT_EALIGN;
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
-    hipLaunchKernelGGL(k_col_inv, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
+    hipLaunchKernelGGL(k_col_inv, dim3((unsigned)(batch * kInvWgs)), dim3(kInvThreads), 0, stream,
                        reinterpret_cast<const float2*>(f), reinterpret_cast<float2*>(work),
                        reinterpret_cast<const float2*>(tab->tw_pass),
                        reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const int*>(ovf), tws);

@@ -12,7 +12,7 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 PLANAR = 0
 INTERLEAVED = 1
 

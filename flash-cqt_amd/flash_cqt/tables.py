@@ -22,14 +22,16 @@ Everything the kernels need that does not depend on the batch:
            rfft is (N/2) irfft with bins 0 and L doubled, of a conj tap the
            conjugate, of the band's 1/M inverse DFT the forward DFT / M.
            Scatter without atomics: the live taps of one bin (at most 4) are
-           ranked; ranks 0 and 1 own the bin's two dense slots (F[2 bin + r]),
-           ranks 2-3 own two slots of a compact overflow area indexed by the
-           bin's position among the bins of degree > 2. Every slot has one
-           writer, the set of written slots is fixed by the table, and slots
-           never written stay zero, so F needs zeroing only once.
-  ovf_*    per scatter table, int32 [16][128] fold lists for the inverse
-           column pass: workgroup w (columns 8w..8w+7 and their mirrors) adds
-           the overflow slots of the bins of degree > 2 in its columns;
+           ranked; ranks 0 and 1 own the bin's slot in dense plane 0 or 1
+           (F[r FSTRIDE + bin]: the taps of one band and rank are contiguous,
+           so a band writes whole cache lines), ranks 2-3 own two slots of a
+           compact overflow area indexed by the bin's position among the bins
+           of degree > 2. Every slot has one writer, the set of written slots
+           is fixed by the table, and slots never written stay zero, so F
+           needs zeroing only once.
+  ovf_*    per scatter table, int32 [8][256] fold lists for the inverse
+           column pass: workgroup w (columns 16w..16w+15 and their mirrors)
+           adds the overflow slots of the bins of degree > 2 in its columns;
            entry = bin | overflow index << 16, -1 = none.
   tasks    band tasks {M, first coefficient, band count, first band}:
            consecutive bands of one group, at most POINTS / M per task.
@@ -49,7 +51,9 @@ L = N // 2
 FSTRIDE = L + 64            # complex elements per half-spectrum plane (>= L + 1)
 OVF_CAP = 1024              # bins with more than two contributing taps, per table
 FROW = 2 * FSTRIDE + 2 * OVF_CAP   # complex elements per batch row of F
-FOLD_PER_WG = 128           # fold-list entries per inverse column workgroup (16 per slice)
+INV_COLS_PER_WG = 32        # inverse column pass: 16 columns + their 16 mirrors per workgroup
+INV_WGS = 256 // INV_COLS_PER_WG    # 8 inverse column workgroups per slice
+FOLD_PER_WG = 256           # fold-list entries per inverse column workgroup (one per thread)
 XSTRIDE = L + 64            # complex elements per row of the real-FFT spectrum X
 POINTS_PER_TASK = 2048      # 128 threads x 16 values per band workgroup
 STAGE_ORDER = ((16, 2), (16, 4), (16, 8), (16, 16), (256, 2), (256, 4), (256, 8))
@@ -181,7 +185,7 @@ def scatter_table(bins, gr, gi):
     without slot).
 
     Live taps (gr or gi nonzero) are ranked per bin in coefficient order;
-    target = 2 bin + rank for ranks 0-1, and
+    target = rank FSTRIDE + bin for ranks 0-1 (dense planes), and
     2 FSTRIDE + 2 * overflow_index(bin) + rank - 2 for ranks 2-3."""
     bins = np.asarray(bins, dtype=np.int64)
     n = bins.size
@@ -201,7 +205,7 @@ def scatter_table(bins, gr, gi):
     oidx = np.full(L + 1, -1, dtype=np.int64)
     oidx[obins] = np.arange(obins.size)
     target = np.zeros(n, dtype=np.int64)
-    tl = np.where(rank < 2, 2 * sb + rank, 2 * FSTRIDE + 2 * oidx[sb] + (rank - 2))
+    tl = np.where(rank < 2, rank * FSTRIDE + sb, 2 * FSTRIDE + 2 * oidx[sb] + (rank - 2))
     target[order] = tl
     assert target.max() < FROW
     gr = np.where(live, gr, 0.0)
@@ -218,19 +222,19 @@ def scatter_table(bins, gr, gi):
 
 def inverse_column_wg(col):
     """Workgroup of the inverse column pass that owns column col (0..255):
-    workgroup w holds columns 8w..8w+7 and their mirrors 256 - p; pair 0
+    workgroup w holds columns 16w..16w+15 and their mirrors 256 - p; pair 0
     is {0, 128}."""
     p = col if col < 128 else (0 if col == 128 else 256 - col)
-    return p // 8
+    return p // 16
 
 
 def fold_lists(obins):
     """Per inverse-column workgroup list of (bin | overflow index << 16)."""
-    lists = [[] for _ in range(16)]
+    lists = [[] for _ in range(INV_WGS)]
     for k, b in enumerate(np.asarray(obins).tolist()):
         w = 0 if b == L else inverse_column_wg(b & 255)
         lists[w].append(b | (k << 16))
-    out = np.full((16, FOLD_PER_WG), -1, dtype=np.int64)
+    out = np.full((INV_WGS, FOLD_PER_WG), -1, dtype=np.int64)
     for w, lst in enumerate(lists):
         assert len(lst) <= FOLD_PER_WG, "fold list overflow"
         out[w, :len(lst)] = lst

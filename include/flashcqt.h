@@ -34,14 +34,14 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 2
+#define FCQT_ABI_VERSION 3
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
 #define FCQT_FSTRIDE 32832    /* complex elements per half-spectrum plane (>= L+1) */
 #define FCQT_OVF_CAP 1024     /* overflow bins (more than two taps) per scatter table */
-#define FCQT_FROW 67712       /* complex elements per batch row of F: 2 slots per bin + 2 x FCQT_OVF_CAP */
-#define FCQT_OVF_LEN 2048     /* int32 entries of a scatter table's overflow fold lists [16][128] */
+#define FCQT_FROW 67712       /* complex elements per batch row of F: 2 slot planes of FCQT_FSTRIDE + 2 x FCQT_OVF_CAP */
+#define FCQT_OVF_LEN 2048     /* int32 entries of a scatter table's overflow fold lists [8][256] */
 #define FCQT_XSTRIDE 32832    /* complex elements per batch row of the real-FFT spectrum X (>= L+1) */
 #define FCQT_TW_STAGE_LEN 4064 /* complex elements of the stage twiddle table */
 #define FCQT_TW_PASS_LEN 32768 /* complex elements of the pass twiddle table [128][256] */
@@ -109,9 +109,9 @@ int fcqt_route_bands(const fcqt_tables* tab, const float* weights, const float* 
  *   D_b = DFT_{M_b}(C_b);  slot(j) of F <- (gr_j Re D_b[j], gi_j Im D_b[j])
  * with one 8-byte record {slot | mode << 30, gr} per tap: gi = gr (mode 0),
  * -gr (mode 1) or 0 (mode 2); gr = 0 skips a tap.
- * F holds, per batch row, two slots per bin for FCQT_FSTRIDE bins
- * (F[2 bin], F[2 bin + 1]) and an overflow area of 2 x FCQT_OVF_CAP slots; a
- * bin's value is the sum of its slots. The
+ * F holds, per batch row, two dense slot planes of FCQT_FSTRIDE bins
+ * (F[bin], F[FCQT_FSTRIDE + bin]) and an overflow area of 2 x FCQT_OVF_CAP
+ * slots; a bin's value is the sum of its slots. The
  * table gives every live tap its own slot (no atomics: results are bitwise
  * reproducible), and the set of slots it writes is fixed, so
  *   - f must be zero-filled once when allocated (fcqt_fill_zero),
@@ -128,7 +128,7 @@ int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat /* [ncoef][2]
  * is the sum of its scatter slots (imaginary parts of bins 0 and 32768
  * ignored, as irfft does). F is read only.
  *   ovf  [FCQT_OVF_LEN] int32 overflow fold lists of the scatter table that
- *        filled F: for each of the 16 column workgroups, up to 128 entries
+ *        filled F: for each of the 8 column workgroups, up to 256 entries
  *        bin | overflow index << 16 (-1 = none)
  *   f    [batch][FCQT_FROW] complex
  *   y    [batch][65536] fp32 out (8-byte aligned)

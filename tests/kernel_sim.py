@@ -228,13 +228,13 @@ def _row_pass(Y, inverse):
 
 
 def staged_bins(Fs, fold):
-    """Bin values [L+1] as k_col_inv stages them: dense slots 2 bin, 2 bin + 1,
-    plus the two overflow slots of every bin on a workgroup's fold list
-    (each listed bin once, owned by the workgroup of its column)."""
-    dense = Fs[0:2 * (L + 1):2] + Fs[1:2 * (L + 1):2]
+    """Bin values [L+1] as k_col_inv stages them: dense slots bin and
+    FSTRIDE + bin, plus the two overflow slots of every bin on a workgroup's
+    fold list (each listed bin once, owned by the workgroup of its column)."""
+    dense = Fs[0:L + 1] + Fs[T.FSTRIDE:T.FSTRIDE + L + 1]
     out = dense.copy()
     seen = set()
-    for w in range(16):
+    for w in range(T.INV_WGS):
         for ent in fold[w * T.FOLD_PER_WG:(w + 1) * T.FOLD_PER_WG].tolist():
             if ent < 0:
                 continue
@@ -248,8 +248,8 @@ def staged_bins(Fs, fold):
 
 
 def inv_col(w, c):
-    p = 8 * w + (c & 7)
-    return p if c < 8 else (128 if p == 0 else 256 - p)
+    p = 16 * w + (c & 15)
+    return p if c < 16 else (128 if p == 0 else 256 - p)
 
 
 def packed_fft_inv(F, ovf=None):
@@ -267,13 +267,13 @@ def packed_fft_inv(F, ovf=None):
         Fb = F[b] if ovf is None else staged_bins(F[b], ovf)
         get = lambda i: Fb[i]
         nyq = get(np.array([L]))[0]
-        for w in range(16):
-            cols = np.array([inv_col(w, c) for c in range(16)])
+        for w in range(T.INV_WGS):
+            cols = np.array([inv_col(w, c) for c in range(T.INV_COLS_PER_WG)])
             raw = get(256 * n1s[None, :] + cols[:, None])       # staged [c][n1]
-            v = np.empty((16, 8, 16), dtype=np.complex128)
+            v = np.empty((T.INV_COLS_PER_WG, 8, 16), dtype=np.complex128)
             for r in range(16):
                 n1 = tt + 8 * r
-                for c in range(16):
+                for c in range(T.INV_COLS_PER_WG):
                     col = cols[c]
                     i = 256 * n1 + col
                     f0 = raw[c, n1].copy()
@@ -282,8 +282,8 @@ def packed_fft_inv(F, ovf=None):
                     elif col == 128:
                         f1 = raw[c, 127 - n1]
                     else:
-                        assert cols[c ^ 8] == 256 - col
-                        f1 = raw[c ^ 8, 127 - n1]
+                        assert cols[c ^ 16] == 256 - col
+                        f1 = raw[c ^ 16, 127 - n1]
                     f1 = f1.copy()
                     zero = i == 0
                     f0[zero] = f0[zero].real

@@ -94,10 +94,11 @@ def test_inverse_tail_matches_irfft(fused, B):
     F = (rs.standard_normal((B, L + 1)) + 1j * rs.standard_normal((B, L + 1))).astype(np.complex64)
     a = (rs.uniform(size=(B, L + 1))).astype(np.float32)
     f = torch.zeros(B, T.FROW, 2, device=_dev())
-    f[:, 0:2 * (L + 1):2, 0] = gpu(F.real * a)
-    f[:, 0:2 * (L + 1):2, 1] = gpu(F.imag * a)
-    f[:, 1:2 * (L + 1):2, 0] = gpu(F.real * (1 - a))
-    f[:, 1:2 * (L + 1):2, 1] = gpu(F.imag * (1 - a))
+    p1 = slice(T.FSTRIDE, T.FSTRIDE + L + 1)
+    f[:, 0:L + 1, 0] = gpu(F.real * a)
+    f[:, 0:L + 1, 1] = gpu(F.imag * a)
+    f[:, p1, 0] = gpu(F.real * (1 - a))
+    f[:, p1, 1] = gpu(F.imag * (1 - a))
     y = torch.empty(B, N, device=_dev())
     w = fused._workspace(B)
     fused.packed_ifft(f, y, w["W"])

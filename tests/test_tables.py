@@ -114,7 +114,7 @@ def test_scatter_slots_unique_and_fold_lists(factored_tables):
         ents = fold[fold >= 0]
         assert np.array_equal(np.sort(ents >> 16), ks)
         assert np.unique(ents & 0xFFFF).size == ents.size
-        for w in range(16):
+        for w in range(T.INV_WGS):
             for e in fold[w * T.FOLD_PER_WG:(w + 1) * T.FOLD_PER_WG]:
                 if e >= 0 and (e & 0xFFFF) != T.L:
                     assert T.inverse_column_wg(int(e) & 255) == w
