@@ -4,10 +4,15 @@
 
 Output: flash-cqt_amd/flash_cqt/_lib/libflashcqt.so. Flags: -O3 for gfx950,
 packed fp32 instructions disabled (-Xclang -target-feature -Xclang
--packed-fp32-ops), hardware fp32 atomics (-munsafe-fp-atomics; every atomic
-target is ordinary device memory). The host pass warns that it does not know
-the packed-fp32 feature; that warning is harmless.
+-packed-fp32-ops). The host pass warns that it does not know the packed-fp32
+feature; that warning is harmless.
+
+The compiler's kernel resource report (-Rpass-analysis=kernel-resource-usage)
+is parsed on every build: a kernel that uses scratch memory (register spills
+or a private array the compiler could not keep in registers) fails the
+build, since every kernel here is meant to run out of registers and LDS.
 """
+import re
 import os
 import pathlib
 import shutil
@@ -31,8 +36,24 @@ def hipcc():
 def command(out=OUT):
     return [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-munsafe-fp-atomics", "-Wall", "-Wno-unused-command-line-argument",
+            "-Rpass-analysis=kernel-resource-usage", "-Wall", "-Wno-unused-command-line-argument",
             *[str(CSRC / s) for s in SOURCES], "-o", str(out)]
+
+
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|LDS Size \[bytes/block\]|"
+                     r"Occupancy \[waves/SIMD\]):\s+(\S+)")
+
+
+def resource_usage(text):
+    """{kernel: {field: value}} from the kernel-resource-usage remarks."""
+    out, cur = {}, None
+    for m in _REMARK.finditer(text):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[key.split(" [")[0]] = int(val)
+    return out
 
 
 def build(verbose=False):
@@ -40,13 +61,23 @@ def build(verbose=False):
     tmp = OUT.with_suffix(".so.tmp")
     cmd = command(tmp)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    lines = [ln for ln in (res.stdout + res.stderr).splitlines()
-             if "packed-fp32-ops' is not a recognized feature" not in ln]
+    text = res.stdout + res.stderr
+    lines = [ln for ln in text.splitlines()
+             if "packed-fp32-ops' is not a recognized feature" not in ln and "remark:" not in ln]
     if verbose or res.returncode != 0:
         print(" ".join(cmd))
         print("\n".join(lines))
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode})")
+    usage = resource_usage(text)
+    if not usage:
+        raise RuntimeError("hipcc printed no kernel resource report")
+    spilled = {k: v for k, v in usage.items() if v.get("ScratchSize", 0) > 0}
+    if spilled:
+        raise RuntimeError(f"kernels use scratch memory: {spilled}")
+    with open(OUT.parent / "resources.txt", "w") as f:
+        for k, v in sorted(usage.items()):
+            f.write(k + " " + " ".join(f"{a}={b}" for a, b in v.items()) + "\n")
     os.replace(tmp, OUT)
     return OUT
 

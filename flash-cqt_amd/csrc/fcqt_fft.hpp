@@ -204,9 +204,37 @@ struct Plan {
 // M/R is a multiple of 16 in every stage that reads LDS, so
 // pad16(j + r M/R) = pad16(j) + r (M/R)(17/16): one address per butterfly,
 // constant offsets for r (immediate offsets of the LDS instructions).
-template <int M, int R, int NS, int SIGN>
+// Stage twiddles of one thread, loaded ahead of the transform (the pass
+// kernels issue them with their data loads, so no table read waits behind a
+// barrier). a: the second stage's Q2 x R2 values, b: the third stage's.
+template <int M>
+struct UnitTw {
+    float2 a[16];
+    float2 b[Plan<M>::R3 > 1 ? 16 : 1];
+};
+
+template <int M>
+__device__ __forceinline__ void load_unit_tw(UnitTw<M>& u, int t, const float2* __restrict__ tws) {
+    using P = Plan<M>;
+    constexpr int T = M / 16;
+#pragma unroll
+    for (int q = 0; q < 16 / P::R2; ++q) {
+        const int k = (t + T * q) & 15;
+        load_tw<P::R2>(u.a + q * P::R2, tws + tw_off(16, P::R2) + k * P::R2);
+    }
+    if constexpr (P::R3 > 1) {
+#pragma unroll
+        for (int q = 0; q < 16 / P::R3; ++q) {
+            const int k = (t + T * q) & 255;
+            load_tw<P::R3>(u.b + q * P::R3, tws + tw_off(256, P::R3) + k * P::R3);
+        }
+    }
+}
+
+template <int M, int R, int NS, int SIGN, bool PRE = false>
 __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
-                                           const float2* __restrict__ tws) {
+                                           const float2* __restrict__ tws,
+                                           const float2* pre = nullptr) {
     constexpr int T = M / 16;
     constexpr int Q = 16 / R;
     constexpr int STRIDE = M / R;
@@ -220,9 +248,13 @@ __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
 #pragma unroll
         for (int r = 0; r < R; ++r) a[r] = sj[r * PSTRIDE];
         if constexpr (NS > 1) {
-            const int k = j & (NS - 1);
             float2 w[R];
-            load_tw<R>(w, tws + tw_off(NS, R) + k * R);
+            if constexpr (PRE) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) w[r] = pre[q * R + r];
+            } else {
+                load_tw<R>(w, tws + tw_off(NS, R) + (j & (NS - 1)) * R);
+            }
 #pragma unroll
             for (int r = 1; r < R; ++r) a[r] = SIGN < 0 ? cmul(a[r], w[r]) : cmulc(a[r], w[r]);
         }
@@ -268,6 +300,22 @@ __device__ __forceinline__ void fft_unit(float2* v, float2* s, int t,
         stage_write<M, 16, 16>(v, s, t);
         __syncthreads();
         stage_read<M, P::R3, 256, SIGN>(v, s, t, tws);
+    }
+}
+
+// The same transform with the stage twiddles preloaded by load_unit_tw.
+template <int M, int SIGN>
+__device__ __forceinline__ void fft_unit(float2* v, float2* s, int t, const UnitTw<M>& pre) {
+    using P = Plan<M>;
+    dft16<SIGN>(v);
+    stage_write<M, 16, 1>(v, s, t);
+    __syncthreads();
+    stage_read<M, P::R2, 16, SIGN, true>(v, s, t, nullptr, pre.a);
+    if constexpr (P::R3 > 1) {
+        __syncthreads();
+        stage_write<M, 16, 16>(v, s, t);
+        __syncthreads();
+        stage_read<M, P::R3, 256, SIGN, true>(v, s, t, nullptr, pre.b);
     }
 }
 

@@ -61,7 +61,15 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
     const float2* xb = in + (long)b * kL;
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
-    fft_unit<128, -1>(v, lds + c * P::US, t, tws);
+    // every twiddle this thread needs, in flight with the data
+    UnitTw<128> utw;
+    load_unit_tw<128>(utw, t, tws);
+    float2 tp[16];
+#pragma unroll
+    for (int q = 0; q < P::QL; ++q)
+#pragma unroll
+        for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + n2];
+    fft_unit<128, -1>(v, lds + c * P::US, t, utw);
     // v[q*8 + r] = V[k1], k1 = t + 8 q + 16 r
     float2* yb = out + (long)b * kL;
 #pragma unroll
@@ -69,8 +77,7 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) {
             const int k1 = t + 8 * q + 16 * r;
-            const int o = k1 * 256 + n2;
-            yb[o] = cmul(v[q * P::RL + r], twp[o]);
+            yb[k1 * 256 + n2] = cmul(v[q * P::RL + r], tp[q * P::RL + r]);
         }
     }
 }
@@ -106,6 +113,12 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
         q0[r] = fb[256 * (t + 8 * r) + col];
         q1[r] = fb[kFStride + 256 * (t + 8 * r) + col];
     }
+    // retangle and pass twiddles, in flight with the data
+    float2 tn[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tn[r] = twn[256 * (t + 8 * r) + col];
+    UnitTw<128> utw;
+    load_unit_tw<128>(utw, t, tws);
     float2 oadd = make_float2(0.0f, 0.0f);
     int opos = -1;
     if (ent >= 0) {
@@ -143,26 +156,29 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int n1 = t + 8 * r;
-        const int i = 256 * n1 + col;
         const float2 f0 = raw[n1];
         const float2 f1 = mp[moff - n1];
         // 2W = conj(S + i D conj(W_N^i)) with S = f0 + conj f1, D = f0 - conj f1;
         // the factor 2 is removed by the 1/(2L) of the unpack
         const float2 sm = make_float2(f0.x + f1.x, f0.y - f1.y);
         const float2 d = make_float2(f0.x - f1.x, f0.y + f1.y);
-        const float2 o = cmulc(d, twn[i]);
+        const float2 o = cmulc(d, tn[r]);
         v[r] = make_float2(sm.x - o.y, -(sm.y + o.x));
     }
+    float2 tp[16];
+#pragma unroll
+    for (int q = 0; q < P::QL; ++q)
+#pragma unroll
+        for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + col];
     __syncthreads();  // staged bins fully consumed before the FFT reuses LDS
-    fft_unit<128, -1>(v, lds + c * P::US, t, tws);
+    fft_unit<128, -1>(v, lds + c * P::US, t, utw);
     float2* yb = out + (long)b * kL;
 #pragma unroll
     for (int q = 0; q < P::QL; ++q) {
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) {
             const int k1 = t + 8 * q + 16 * r;
-            const int o = k1 * 256 + col;
-            yb[o] = cmul(v[q * P::RL + r], twp[o]);
+            yb[k1 * 256 + col] = cmul(v[q * P::RL + r], tp[q * P::RL + r]);
         }
     }
 }
@@ -179,14 +195,23 @@ __device__ __forceinline__ int fwd_row(int w, int rho) {
 
 // Row FFTs of one 16-row tile, results left in LDS as Z_row[k2] at
 // lds[rho*US + pad16(k2)] (a barrier follows).
+// hold: values loaded before the call that must arrive with the row data
+// (the untangle twiddles), so they are not deferred past the barriers.
+template <bool HOLD>
 __device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, float2* lds, int rho, int t,
-                                               const float2* __restrict__ tws) {
+                                               const float2* __restrict__ tws, float2* hold) {
     using P = Plan<256>;
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = yrow[t + 16 * r];
+    UnitTw<256> utw;
+    load_unit_tw<256>(utw, t, tws);
+    if constexpr (HOLD) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) asm volatile("" : "+v"(hold[u].x), "+v"(hold[u].y));
+    }
     float2* s = lds + rho * P::US;
-    fft_unit<256, -1>(v, s, t, tws);
+    fft_unit<256, -1>(v, s, t, utw);
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[pad16(t + 16 * r)] = v[r];
@@ -209,7 +234,7 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
     float2 wn[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) wn[u] = twn[k1 + 128 * (kg + 16 * u)];
-    row_fft_to_lds(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, rho, t, tws);
+    row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, rho, t, tws, wn);
     // untangle: lanes walk the tile's rows for coalesced stores
     const float2* s = lds + rho2 * P::US;
     // mirror bin L - k: row 128 - k1 at column 255 - k2; rows 0 and 64 are
@@ -242,7 +267,7 @@ __global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, 
     const int rg = blockIdx.x - b * kRowWgs;
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
-    row_fft_to_lds(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, rho, t, tws);
+    row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, rho, t, tws, nullptr);
     const int rho2 = threadIdx.x & 15;
     const int kg = threadIdx.x >> 4;
     const float2* s2 = lds + rho2 * P::US;
