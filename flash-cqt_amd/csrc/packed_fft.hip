@@ -52,8 +52,9 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
                                                  const float2* __restrict__ tws) {
     using P = Plan<128>;
     __shared__ float2 lds[kColsPerWg * P::US];
-    const int b = blockIdx.x / kColWgs;
-    const int cg = blockIdx.x - b * kColWgs;
+    const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int b = lg / kColWgs;
+    const int cg = lg - b * kColWgs;
     const int c = threadIdx.x & (kColsPerWg - 1);  // column within the tile
     const int t = threadIdx.x >> 4;                // thread within the column FFT, < 8
     const int n2 = cg * kColsPerWg + c;
@@ -98,8 +99,9 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
                                                          const float2* __restrict__ tws) {
     using P = Plan<128>;
     __shared__ float2 lds[kInvColsPerWg * P::US];  // staged bins, then FFT exchange
-    const int b = blockIdx.x / kInvWgs;
-    const int w = blockIdx.x - b * kInvWgs;
+    const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int b = lg / kInvWgs;
+    const int w = lg - b * kInvWgs;
     const int c = threadIdx.x & (kInvColsPerWg - 1);
     const int t = threadIdx.x >> 5;
     const int col = inv_col(w, c);
@@ -223,8 +225,9 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
                                                  const float2* __restrict__ tws) {
     using P = Plan<256>;
     __shared__ float2 lds[kRowsPerWg * P::US];
-    const int b = blockIdx.x / kRowWgs;
-    const int w = blockIdx.x - b * kRowWgs;
+    const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int b = lg / kRowWgs;
+    const int w = lg - b * kRowWgs;
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
     // untangle twiddles of this thread's output bins, loaded up front
@@ -263,8 +266,9 @@ __global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, 
                                                  const float2* __restrict__ tws) {
     using P = Plan<256>;
     __shared__ float2 lds[kRowsPerWg * P::US];
-    const int b = blockIdx.x / kRowWgs;
-    const int rg = blockIdx.x - b * kRowWgs;
+    const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int b = lg / kRowWgs;
+    const int rg = lg - b * kRowWgs;
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
     row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, rho, t, tws, nullptr);
