@@ -165,22 +165,22 @@ __device__ __forceinline__ void dft(float2* a) {
 
 // ------------------------------------------------------- stage twiddles
 // Table layout (complex, forward sign): for each (NS, R) in the order below,
-// entry [k][r] = W_{NS R}^{r k}, k < NS, r < R. Offsets in complex elements.
+// entry [r][k] = W_{NS R}^{r k}, r < R, k < NS. The lanes of one load share r
+// and hold consecutive k, so every load touches few cache lines. Offsets in
+// complex elements.
 constexpr int tw_off(int NS, int R) {
     return NS == 16 ? (R == 2 ? 0 : R == 4 ? 32 : R == 8 ? 96 : 224)
                     : (R == 2 ? 480 : R == 4 ? 992 : 2016);
 }
 constexpr int kTwStageLen = 4064;
 
-template <int R>
-__device__ __forceinline__ void load_tw(float2* w, const float2* __restrict__ row) {
-    const float4* p = reinterpret_cast<const float4*>(row);
+// w[r] = W_{NS R}^{r k} for r = 1..R-1 (w[0] = 1 is never read).
+template <int NS, int R>
+__device__ __forceinline__ void load_tw(float2* w, const float2* __restrict__ tws, int k) {
+    const float2* col = tws + tw_off(NS, R) + k;
+    w[0] = make_float2(1.0f, 0.0f);
 #pragma unroll
-    for (int i = 0; i < R / 2; ++i) {
-        const float4 q = p[i];
-        w[2 * i] = make_float2(q.x, q.y);
-        w[2 * i + 1] = make_float2(q.z, q.w);
-    }
+    for (int r = 1; r < R; ++r) w[r] = col[r * NS];
 }
 
 // ------------------------------------------------------------ the plan
@@ -218,16 +218,10 @@ __device__ __forceinline__ void load_unit_tw(UnitTw<M>& u, int t, const float2* 
     using P = Plan<M>;
     constexpr int T = M / 16;
 #pragma unroll
-    for (int q = 0; q < 16 / P::R2; ++q) {
-        const int k = (t + T * q) & 15;
-        load_tw<P::R2>(u.a + q * P::R2, tws + tw_off(16, P::R2) + k * P::R2);
-    }
+    for (int q = 0; q < 16 / P::R2; ++q) load_tw<16, P::R2>(u.a + q * P::R2, tws, (t + T * q) & 15);
     if constexpr (P::R3 > 1) {
 #pragma unroll
-        for (int q = 0; q < 16 / P::R3; ++q) {
-            const int k = (t + T * q) & 255;
-            load_tw<P::R3>(u.b + q * P::R3, tws + tw_off(256, P::R3) + k * P::R3);
-        }
+        for (int q = 0; q < 16 / P::R3; ++q) load_tw<256, P::R3>(u.b + q * P::R3, tws, (t + T * q) & 255);
     }
 }
 
@@ -253,7 +247,7 @@ __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
 #pragma unroll
                 for (int r = 0; r < R; ++r) w[r] = pre[q * R + r];
             } else {
-                load_tw<R>(w, tws + tw_off(NS, R) + (j & (NS - 1)) * R);
+                load_tw<NS, R>(w, tws, j & (NS - 1));
             }
 #pragma unroll
             for (int r = 1; r < R; ++r) a[r] = SIGN < 0 ? cmul(a[r], w[r]) : cmulc(a[r], w[r]);

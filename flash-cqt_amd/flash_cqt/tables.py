@@ -37,8 +37,10 @@ Everything the kernels need that does not depend on the batch:
            consecutive bands of one group, at most POINTS / M per task.
   tw_pass  W_L^(k1 n2) at k1*256 + n2 (column pass of the packed FFT).
   tw_half  W_N^i, i < L (retangle of the inverse).
-  tw_stage Stockham stage twiddles W_{NS R}^(r k) in [k][r] rows for
-           (NS, R) = (16,2) (16,4) (16,8) (16,16) (256,2) (256,4) (256,8).
+  tw_stage Stockham stage twiddles W_{NS R}^(r k) in [r][k] rows for
+           (NS, R) = (16,2) (16,4) (16,8) (16,16) (256,2) (256,4) (256,8):
+           the lanes of one load share r and take consecutive k, so a load
+           touches one 128-byte line per 16 lanes.
 Semantics follow fused.py:303-476 (records, adjoint constants); the layout
 (natural order, folded scales, 64-lane-friendly rows) is this engine's own.
 Every angle is taken from an exact integer residue in float64 and rounded
@@ -80,9 +82,9 @@ def _bits(f):
 def stage_twiddles():
     rows = []
     for ns, r in STAGE_ORDER:
-        k = np.arange(ns)[:, None]
-        rr = np.arange(r)[None, :]
-        rows.append(_unit_roots(k * rr, ns * r).reshape(-1))
+        rr = np.arange(r)[:, None]
+        k = np.arange(ns)[None, :]
+        rows.append(_unit_roots(rr * k, ns * r).reshape(-1))
     out = np.concatenate(rows)
     assert out.size == TW_STAGE_LEN
     return _as_pairs(out)

@@ -86,7 +86,7 @@ def stage_read(s, t, M, R, NS, sign, base):
         if NS > 1:
             k = j & (NS - 1)
             off = tw_off(NS, R)
-            rows = off + k[:, None] * R + np.arange(R)[None, :]
+            rows = off + np.arange(R)[None, :] * NS + k[:, None]
             assert rows.max() < T.TW_STAGE_LEN
             w = tws()[rows]
             if sign > 0:
