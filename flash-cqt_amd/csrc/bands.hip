@@ -57,8 +57,10 @@ template <int M, int LAYOUT>
 __device__ __forceinline__ void route_band(const int4 task, const int b, const float2* __restrict__ xs,
                                            float* __restrict__ cre, float* __restrict__ cim,
                                            const float* __restrict__ wt, const int4* __restrict__ bands,
-                                           const long ncoef, const float2* __restrict__ tws, float2* lds) {
+                                           const long ncoef, const float2* __restrict__ tws, float2* lds,
+                                           float2* tw2) {
     using P = Plan<M>;
+    load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
@@ -111,7 +113,7 @@ __device__ __forceinline__ void route_band(const int4 task, const int b, const f
         for (int r = 0; r < 16; ++r)
             v[r] = make_float2(w[r] * xv[r].x, (cj >> r) & 1u ? -w[r] * xv[r].y : w[r] * xv[r].y);
     }
-    fft_unit<M, +1>(v, lds + u * P::US, t, tws);
+    fft_unit<M, +1>(v, lds + u * P::US, t, tws, tw2);
     if (active) {
         const long ob = (long)b * ncoef + task.y;           // uniform
 #pragma unroll
@@ -130,8 +132,9 @@ template <int M, int LAYOUT>
 __device__ __forceinline__ void scatter_band(const int4 task, const int b, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
                                              const int2* __restrict__ scat, const long ncoef,
-                                             const float2* __restrict__ tws, float2* lds) {
+                                             const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
+    load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
@@ -142,7 +145,7 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, ub + t + P::T * r);
-    fft_unit<M, -1>(v, lds + u * P::US, t, tws);
+    fft_unit<M, -1>(v, lds + u * P::US, t, tws, tw2);
     // records {slot | mode << 30, gain}: mode 0 gi = gr, 1 gi = -gr, 2 gi = 0;
     // gain 0 = no slot. All 16 loads issue before the first store.
     const int2* st = scat + task.y;                        // uniform
@@ -181,17 +184,18 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
                                                               const int4* __restrict__ tasks, int batch,
                                                               long ncoef, const float2* __restrict__ tws) {
     __shared__ float2 lds[kBandLds];
+    __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
     decode_task(batch, task_id, b);
     const int4 td = tasks[task_id];
     switch (td.x) {
-        case 32: route_band<32, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
-        case 64: route_band<64, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
-        case 128: route_band<128, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
-        case 256: route_band<256, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
-        case 512: route_band<512, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
-        case 1024: route_band<1024, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
-        case 2048: route_band<2048, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds); break;
+        case 32: route_band<32, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
+        case 64: route_band<64, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
+        case 128: route_band<128, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
+        case 256: route_band<256, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
+        case 512: route_band<512, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
+        case 1024: route_band<1024, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
+        case 2048: route_band<2048, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
         default: break;
     }
 }
@@ -204,17 +208,18 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
                                                                 const int4* __restrict__ tasks, int batch,
                                                                 long ncoef, const float2* __restrict__ tws) {
     __shared__ float2 lds[kBandLds];
+    __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
     decode_task(batch, task_id, b);
     const int4 td = tasks[task_id];
     switch (td.x) {
-        case 32: scatter_band<32, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
-        case 64: scatter_band<64, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
-        case 128: scatter_band<128, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
-        case 256: scatter_band<256, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
-        case 512: scatter_band<512, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
-        case 1024: scatter_band<1024, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
-        case 2048: scatter_band<2048, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds); break;
+        case 32: scatter_band<32, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
+        case 64: scatter_band<64, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
+        case 128: scatter_band<128, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
+        case 256: scatter_band<256, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
+        case 512: scatter_band<512, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
+        case 1024: scatter_band<1024, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
+        case 2048: scatter_band<2048, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
         default: break;
     }
 }

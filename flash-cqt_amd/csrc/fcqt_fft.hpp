@@ -174,15 +174,6 @@ constexpr int tw_off(int NS, int R) {
 }
 constexpr int kTwStageLen = 4064;
 
-// w[r] = W_{NS R}^{r k} for r = 1..R-1 (w[0] = 1 is never read).
-template <int NS, int R>
-__device__ __forceinline__ void load_tw(float2* w, const float2* __restrict__ tws, int k) {
-    const float2* col = tws + tw_off(NS, R) + k;
-    w[0] = make_float2(1.0f, 0.0f);
-#pragma unroll
-    for (int r = 1; r < R; ++r) w[r] = col[r * NS];
-}
-
 // ------------------------------------------------------------ the plan
 
 __device__ __forceinline__ int pad16(int i) { return i + (i >> 4); }
@@ -199,36 +190,54 @@ struct Plan {
     static constexpr int US = M + M / 16 + 1;            // LDS stride per unit (complex)
 };
 
+// Twiddle sources. The second stage (NS = 16) takes its W_{16 R}^{r k}
+// from a copy of its table block in LDS (16 R values, [r][k]): one copy per
+// workgroup, and no vector-memory instruction per twiddle. The third stage
+// (NS = 256, R <= 8) loads W^k, W^2k and W^4k and forms W^3k, W^5k, W^6k,
+// W^7k as products (at most two roundings more than a table value).
+template <int M>
+constexpr int tw2_len() { return 16 * Plan<M>::R2; }
+
+// Copy the second-stage twiddle block into LDS (tl holds tw2_len<M>()
+// values); every thread of the workgroup calls this before its first
+// barrier.
+template <int M>
+__device__ __forceinline__ void load_tw2_lds(float2* tl, const float2* __restrict__ tws, int tid,
+                                             int nthreads) {
+    constexpr int R = Plan<M>::R2;
+    constexpr int N4 = tw2_len<M>() / 2;
+    const float4* src = reinterpret_cast<const float4*>(tws + tw_off(16, R));
+    float4* dst = reinterpret_cast<float4*>(tl);
+    for (int i = tid; i < N4; i += nthreads) dst[i] = src[i];
+}
+
+template <int R>
+__device__ __forceinline__ void load_tw3(float2* w, const float2* __restrict__ tws, int k) {
+    static_assert(R == 2 || R == 4 || R == 8, "third-stage radix");
+    const float2* col = tws + tw_off(256, R) + k;
+    w[0] = make_float2(1.0f, 0.0f);
+    w[1] = col[256];
+    if constexpr (R >= 4) {
+        w[2] = col[512];
+        w[3] = cmul(w[1], w[2]);
+    }
+    if constexpr (R == 8) {
+        w[4] = col[1024];
+        w[5] = cmul(w[1], w[4]);
+        w[6] = cmul(w[2], w[4]);
+        w[7] = cmul(w[3], w[4]);
+    }
+}
+
 // One Stockham stage read: butterflies j = t + T q, inputs j + r M/R,
 // twiddle W_{NS R}^{r (j mod NS)}, radix-R DFT, results into v[q R + r].
 // M/R is a multiple of 16 in every stage that reads LDS, so
 // pad16(j + r M/R) = pad16(j) + r (M/R)(17/16): one address per butterfly,
 // constant offsets for r (immediate offsets of the LDS instructions).
-// Stage twiddles of one thread, loaded ahead of the transform (the pass
-// kernels issue them with their data loads, so no table read waits behind a
-// barrier). a: the second stage's Q2 x R2 values, b: the third stage's.
-template <int M>
-struct UnitTw {
-    float2 a[16];
-    float2 b[Plan<M>::R3 > 1 ? 16 : 1];
-};
-
-template <int M>
-__device__ __forceinline__ void load_unit_tw(UnitTw<M>& u, int t, const float2* __restrict__ tws) {
-    using P = Plan<M>;
-    constexpr int T = M / 16;
-#pragma unroll
-    for (int q = 0; q < 16 / P::R2; ++q) load_tw<16, P::R2>(u.a + q * P::R2, tws, (t + T * q) & 15);
-    if constexpr (P::R3 > 1) {
-#pragma unroll
-        for (int q = 0; q < 16 / P::R3; ++q) load_tw<256, P::R3>(u.b + q * P::R3, tws, (t + T * q) & 255);
-    }
-}
-
-template <int M, int R, int NS, int SIGN, bool PRE = false>
+// tl: the LDS twiddle block for NS = 16; tws: the table for NS = 256.
+template <int M, int R, int NS, int SIGN>
 __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
-                                           const float2* __restrict__ tws,
-                                           const float2* pre = nullptr) {
+                                           const float2* __restrict__ tws, const float2* tl) {
     constexpr int T = M / 16;
     constexpr int Q = 16 / R;
     constexpr int STRIDE = M / R;
@@ -243,11 +252,13 @@ __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
         for (int r = 0; r < R; ++r) a[r] = sj[r * PSTRIDE];
         if constexpr (NS > 1) {
             float2 w[R];
-            if constexpr (PRE) {
+            if constexpr (NS == 16) {
+                const float2* tk = tl + (j & 15);
+                w[0] = make_float2(1.0f, 0.0f);
 #pragma unroll
-                for (int r = 0; r < R; ++r) w[r] = pre[q * R + r];
+                for (int r = 1; r < R; ++r) w[r] = tk[16 * r];
             } else {
-                load_tw<NS, R>(w, tws, j & (NS - 1));
+                load_tw3<R>(w, tws, j & (NS - 1));
             }
 #pragma unroll
             for (int r = 1; r < R; ++r) a[r] = SIGN < 0 ? cmul(a[r], w[r]) : cmulc(a[r], w[r]);
@@ -278,38 +289,23 @@ __device__ __forceinline__ void stage_write(const float2* v, float2* s, int t) {
 }
 
 // Whole unit transform. Entry: v[r] = x[t + T r]; the unit's LDS region s is
-// free to write. Exit: v[q RL + r] = X[t + T q + r OS]; other threads may
+// free to write; tl holds the second-stage twiddle block (load_tw2_lds
+// before the call). Exit: v[q RL + r] = X[t + T q + r OS]; other threads may
 // still read s, so a caller that writes s again must barrier first.
 // Every thread of the workgroup must call this (it contains barriers).
 template <int M, int SIGN>
-__device__ __forceinline__ void fft_unit(float2* v, float2* s, int t,
-                                         const float2* __restrict__ tws) {
+__device__ __forceinline__ void fft_unit(float2* v, float2* s, int t, const float2* __restrict__ tws,
+                                         const float2* tl) {
     using P = Plan<M>;
     dft16<SIGN>(v);
     stage_write<M, 16, 1>(v, s, t);
     __syncthreads();
-    stage_read<M, P::R2, 16, SIGN>(v, s, t, tws);
+    stage_read<M, P::R2, 16, SIGN>(v, s, t, tws, tl);
     if constexpr (P::R3 > 1) {
         __syncthreads();
         stage_write<M, 16, 16>(v, s, t);
         __syncthreads();
-        stage_read<M, P::R3, 256, SIGN>(v, s, t, tws);
-    }
-}
-
-// The same transform with the stage twiddles preloaded by load_unit_tw.
-template <int M, int SIGN>
-__device__ __forceinline__ void fft_unit(float2* v, float2* s, int t, const UnitTw<M>& pre) {
-    using P = Plan<M>;
-    dft16<SIGN>(v);
-    stage_write<M, 16, 1>(v, s, t);
-    __syncthreads();
-    stage_read<M, P::R2, 16, SIGN, true>(v, s, t, nullptr, pre.a);
-    if constexpr (P::R3 > 1) {
-        __syncthreads();
-        stage_write<M, 16, 16>(v, s, t);
-        __syncthreads();
-        stage_read<M, P::R3, 256, SIGN, true>(v, s, t, nullptr, pre.b);
+        stage_read<M, P::R3, 256, SIGN>(v, s, t, tws, tl);
     }
 }
 

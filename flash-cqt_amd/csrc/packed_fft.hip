@@ -63,14 +63,14 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
     // every twiddle this thread needs, in flight with the data
-    UnitTw<128> utw;
-    load_unit_tw<128>(utw, t, tws);
+    __shared__ float2 tw2[tw2_len<128>()];
+    load_tw2_lds<128>(tw2, tws, threadIdx.x, 128);
     float2 tp[16];
 #pragma unroll
     for (int q = 0; q < P::QL; ++q)
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + n2];
-    fft_unit<128, -1>(v, lds + c * P::US, t, utw);
+    fft_unit<128, -1>(v, lds + c * P::US, t, tws, tw2);
     // v[q*8 + r] = V[k1], k1 = t + 8 q + 16 r
     float2* yb = out + (long)b * kL;
 #pragma unroll
@@ -119,8 +119,8 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
     float2 tn[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) tn[r] = twn[256 * (t + 8 * r) + col];
-    UnitTw<128> utw;
-    load_unit_tw<128>(utw, t, tws);
+    __shared__ float2 tw2[tw2_len<128>()];
+    load_tw2_lds<128>(tw2, tws, threadIdx.x, kInvThreads);
     float2 oadd = make_float2(0.0f, 0.0f);
     int opos = -1;
     if (ent >= 0) {
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + col];
     __syncthreads();  // staged bins fully consumed before the FFT reuses LDS
-    fft_unit<128, -1>(v, lds + c * P::US, t, utw);
+    fft_unit<128, -1>(v, lds + c * P::US, t, tws, tw2);
     float2* yb = out + (long)b * kL;
 #pragma unroll
     for (int q = 0; q < P::QL; ++q) {
@@ -200,20 +200,19 @@ __device__ __forceinline__ int fwd_row(int w, int rho) {
 // hold: values loaded before the call that must arrive with the row data
 // (the untangle twiddles), so they are not deferred past the barriers.
 template <bool HOLD>
-__device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, float2* lds, int rho, int t,
-                                               const float2* __restrict__ tws, float2* hold) {
+__device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, float2* lds, float2* tw2,
+                                               int rho, int t, const float2* __restrict__ tws, float2* hold) {
     using P = Plan<256>;
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = yrow[t + 16 * r];
-    UnitTw<256> utw;
-    load_unit_tw<256>(utw, t, tws);
+    load_tw2_lds<256>(tw2, tws, threadIdx.x, 256);
     if constexpr (HOLD) {
 #pragma unroll
         for (int u = 0; u < 16; ++u) asm volatile("" : "+v"(hold[u].x), "+v"(hold[u].y));
     }
     float2* s = lds + rho * P::US;
-    fft_unit<256, -1>(v, s, t, utw);
+    fft_unit<256, -1>(v, s, t, tws, tw2);
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[pad16(t + 16 * r)] = v[r];
@@ -225,6 +224,7 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
                                                  const float2* __restrict__ tws) {
     using P = Plan<256>;
     __shared__ float2 lds[kRowsPerWg * P::US];
+    __shared__ float2 tw2[tw2_len<256>()];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int b = lg / kRowWgs;
     const int w = lg - b * kRowWgs;
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
     float2 wn[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) wn[u] = twn[k1 + 128 * (kg + 16 * u)];
-    row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, rho, t, tws, wn);
+    row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, tw2, rho, t, tws, wn);
     // untangle: lanes walk the tile's rows for coalesced stores
     const float2* s = lds + rho2 * P::US;
     // mirror bin L - k: row 128 - k1 at column 255 - k2; rows 0 and 64 are
@@ -266,12 +266,14 @@ __global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, 
                                                  const float2* __restrict__ tws) {
     using P = Plan<256>;
     __shared__ float2 lds[kRowsPerWg * P::US];
+    __shared__ float2 tw2[tw2_len<256>()];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int b = lg / kRowWgs;
     const int rg = lg - b * kRowWgs;
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
-    row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, rho, t, tws, nullptr);
+    row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, tw2, rho, t, tws,
+                          nullptr);
     const int rho2 = threadIdx.x & 15;
     const int kg = threadIdx.x >> 4;
     const float2* s2 = lds + rho2 * P::US;
