@@ -61,6 +61,8 @@ __device__ __forceinline__ void route_band(const int4 task, const int b, const f
                                            float2* tw2) {
     using P = Plan<M>;
     load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
+    Tw3<M> w3;
+    load_tw3<M>(w3, tws, threadIdx.x % P::T);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
@@ -113,7 +115,7 @@ __device__ __forceinline__ void route_band(const int4 task, const int b, const f
         for (int r = 0; r < 16; ++r)
             v[r] = make_float2(w[r] * xv[r].x, (cj >> r) & 1u ? -w[r] * xv[r].y : w[r] * xv[r].y);
     }
-    fft_unit<M, +1>(v, lds + u * P::US, t, tws, tw2);
+    fft_unit<M, +1>(v, lds + u * P::US, t, tw2, w3);
     if (active) {
         const long ob = (long)b * ncoef + task.y;           // uniform
 #pragma unroll
@@ -135,6 +137,8 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
                                              const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
     load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
+    Tw3<M> w3;
+    load_tw3<M>(w3, tws, threadIdx.x % P::T);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
@@ -145,7 +149,7 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, ub + t + P::T * r);
-    fft_unit<M, -1>(v, lds + u * P::US, t, tws, tw2);
+    fft_unit<M, -1>(v, lds + u * P::US, t, tw2, w3);
     // records {slot | mode << 30, gain}: mode 0 gi = gr, 1 gi = -gr, 2 gi = 0;
     // gain 0 = no slot. All 16 loads issue before the first store.
     const int2* st = scat + task.y;                        // uniform

@@ -211,21 +211,47 @@ __device__ __forceinline__ void load_tw2_lds(float2* tl, const float2* __restric
     for (int i = tid; i < N4; i += nthreads) dst[i] = src[i];
 }
 
+// Third-stage bases W^k, W^2k, W^4k (k = j mod 256) of each of a thread's
+// 16 / R3 butterflies, loaded with the unit's data so that no table read
+// waits behind the transform's barriers.
+template <int M>
+struct Tw3 {
+    static constexpr int R = Plan<M>::R3;
+    static constexpr int Q = R > 1 ? 16 / R : 1;
+    float2 b[Q][3];
+};
+
+template <int M>
+__device__ __forceinline__ void load_tw3(Tw3<M>& w3, const float2* __restrict__ tws, int t) {
+    constexpr int R = Plan<M>::R3;
+    if constexpr (R > 1) {
+        static_assert(R == 2 || R == 4 || R == 8, "third-stage radix");
+        constexpr int T = M / 16;
+#pragma unroll
+        for (int q = 0; q < Tw3<M>::Q; ++q) {
+            const float2* col = tws + tw_off(256, R) + ((t + T * q) & 255);
+            w3.b[q][0] = col[256];
+            if constexpr (R >= 4) w3.b[q][1] = col[512];
+            if constexpr (R == 8) w3.b[q][2] = col[1024];
+        }
+    }
+}
+
+// W^{rk}, r < R, from the bases: W^3k, W^5k, W^6k, W^7k as products (at most
+// two roundings more than a table value).
 template <int R>
-__device__ __forceinline__ void load_tw3(float2* w, const float2* __restrict__ tws, int k) {
-    static_assert(R == 2 || R == 4 || R == 8, "third-stage radix");
-    const float2* col = tws + tw_off(256, R) + k;
+__device__ __forceinline__ void expand_tw3(float2* w, const float2* b) {
     w[0] = make_float2(1.0f, 0.0f);
-    w[1] = col[256];
+    w[1] = b[0];
     if constexpr (R >= 4) {
-        w[2] = col[512];
-        w[3] = cmul(w[1], w[2]);
+        w[2] = b[1];
+        w[3] = cmul(b[0], b[1]);
     }
     if constexpr (R == 8) {
-        w[4] = col[1024];
-        w[5] = cmul(w[1], w[4]);
-        w[6] = cmul(w[2], w[4]);
-        w[7] = cmul(w[3], w[4]);
+        w[4] = b[2];
+        w[5] = cmul(b[0], b[2]);
+        w[6] = cmul(b[1], b[2]);
+        w[7] = cmul(w[3], b[2]);
     }
 }
 
@@ -236,8 +262,8 @@ __device__ __forceinline__ void load_tw3(float2* w, const float2* __restrict__ t
 // constant offsets for r (immediate offsets of the LDS instructions).
 // tl: the LDS twiddle block for NS = 16; tws: the table for NS = 256.
 template <int M, int R, int NS, int SIGN>
-__device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
-                                           const float2* __restrict__ tws, const float2* tl) {
+__device__ __forceinline__ void stage_read(float2* v, const float2* s, int t, const float2* tl,
+                                           const Tw3<M>& w3) {
     constexpr int T = M / 16;
     constexpr int Q = 16 / R;
     constexpr int STRIDE = M / R;
@@ -258,7 +284,7 @@ __device__ __forceinline__ void stage_read(float2* v, const float2* s, int t,
 #pragma unroll
                 for (int r = 1; r < R; ++r) w[r] = tk[16 * r];
             } else {
-                load_tw3<R>(w, tws, j & (NS - 1));
+                expand_tw3<R>(w, w3.b[q]);
             }
 #pragma unroll
             for (int r = 1; r < R; ++r) a[r] = SIGN < 0 ? cmul(a[r], w[r]) : cmulc(a[r], w[r]);
@@ -290,22 +316,22 @@ __device__ __forceinline__ void stage_write(const float2* v, float2* s, int t) {
 
 // Whole unit transform. Entry: v[r] = x[t + T r]; the unit's LDS region s is
 // free to write; tl holds the second-stage twiddle block (load_tw2_lds
-// before the call). Exit: v[q RL + r] = X[t + T q + r OS]; other threads may
-// still read s, so a caller that writes s again must barrier first.
+// before the call), w3 the third-stage bases (load_tw3). Exit:
+// v[q RL + r] = X[t + T q + r OS]; other threads may still read s, so a
+// caller that writes s again must barrier first.
 // Every thread of the workgroup must call this (it contains barriers).
 template <int M, int SIGN>
-__device__ __forceinline__ void fft_unit(float2* v, float2* s, int t, const float2* __restrict__ tws,
-                                         const float2* tl) {
+__device__ __forceinline__ void fft_unit(float2* v, float2* s, int t, const float2* tl, const Tw3<M>& w3) {
     using P = Plan<M>;
     dft16<SIGN>(v);
     stage_write<M, 16, 1>(v, s, t);
     __syncthreads();
-    stage_read<M, P::R2, 16, SIGN>(v, s, t, tws, tl);
+    stage_read<M, P::R2, 16, SIGN>(v, s, t, tl, w3);
     if constexpr (P::R3 > 1) {
         __syncthreads();
         stage_write<M, 16, 16>(v, s, t);
         __syncthreads();
-        stage_read<M, P::R3, 256, SIGN>(v, s, t, tws, tl);
+        stage_read<M, P::R3, 256, SIGN>(v, s, t, tl, w3);
     }
 }
 

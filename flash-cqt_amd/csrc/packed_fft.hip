@@ -70,7 +70,7 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
     for (int q = 0; q < P::QL; ++q)
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + n2];
-    fft_unit<128, -1>(v, lds + c * P::US, t, tws, tw2);
+    fft_unit<128, -1>(v, lds + c * P::US, t, tw2, Tw3<128>{});
     // v[q*8 + r] = V[k1], k1 = t + 8 q + 16 r
     float2* yb = out + (long)b * kL;
 #pragma unroll
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + col];
     __syncthreads();  // staged bins fully consumed before the FFT reuses LDS
-    fft_unit<128, -1>(v, lds + c * P::US, t, tws, tw2);
+    fft_unit<128, -1>(v, lds + c * P::US, t, tw2, Tw3<128>{});
     float2* yb = out + (long)b * kL;
 #pragma unroll
     for (int q = 0; q < P::QL; ++q) {
@@ -212,7 +212,7 @@ __device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, 
         for (int u = 0; u < 16; ++u) asm volatile("" : "+v"(hold[u].x), "+v"(hold[u].y));
     }
     float2* s = lds + rho * P::US;
-    fft_unit<256, -1>(v, s, t, tws, tw2);
+    fft_unit<256, -1>(v, s, t, tw2, Tw3<256>{});
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[pad16(t + 16 * r)] = v[r];
