@@ -48,12 +48,12 @@ extern "C" int fcqt_fill_zero(float* buf, int64_t n, hipStream_t stream) {
     return launch_status();
 }
 
-extern "C" int fcqt_analysis(const fcqt_tables* tab, const float* weights, const float* x, float* coef_re,
+extern "C" int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x, float* coef_re,
                              float* coef_im, int layout, float* xs, float* work, int64_t batch,
                              hipStream_t stream) {
-    if (!weights || !x || !xs || !work) return FCQT_EARG;
+    if (!route || !x || !xs || !work) return FCQT_EARG;
     if (int e = fcqt_packed_fft_fwd(tab, x, xs, work, batch, stream)) return e;
-    return fcqt_route_bands(tab, weights, xs, coef_re, coef_im, layout, batch, stream);
+    return fcqt_route_bands(tab, route, xs, coef_re, coef_im, layout, batch, stream);
 }
 
 extern "C" int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* ovf,

@@ -4,23 +4,28 @@
 // One workgroup of 128 threads (two wave64s) owns one task: up to 2048/M
 // consecutive bands of one length M of one slice. Each band is one unit of
 // the shared FFT engine (M/16 threads, 16 values each). Tasks come from a
-// host-built table {M, first coefficient, band count, 0}; the grid is
-// tasks x batch, spread so that each XCD gets a contiguous range of
+// host-built table {M, first coefficient, band count, first band}; the grid
+// is tasks x batch, spread so that each XCD gets a contiguous range of
 // (task, slice) pairs and so reads each task's record rows from one L2.
 //
-// Analysis prologue (tap j of a band): v_j = w_j X[k_j], conjugated for taps
-// past Nyquist, where X is the real FFT of the slice (the forward row pass
-// already untangled the packed spectrum) and w_j one fp32 weight per tap
+// Both engines read their per-tap records in kernel order: the table holds,
+// for every task, 16 rows of 128 8-byte records, row s giving slot s of each
+// thread (the host builds the permutation from the task table). A thread's
+// records therefore sit at task * 2048 + s * 128 + thread: the loads depend
+// on the task index only, issue before the task record arrives, and every
+// load of a wave is one contiguous 512-byte run.
+//
+// Analysis prologue (slot r of a thread = tap t + T r of its band):
+// v = w X[k], conjugated for taps past Nyquist, from the record
+// {k | conj << 31, w}: X is the real FFT of the slice (the forward row pass
+// already untangled the packed spectrum) and w one fp32 weight per tap
 // (window / M for the analysis, dual window * 2/N for the synthesis
-// adjoint). The bin k_j follows from the band's descriptor {c, r, l}: taps
-// j < r read bin c + j, taps j >= M - l read bin c + j - M (mod N, folded
-// past N/2 to N - k with conjugation), the taps between are zero. The index
-// needs no table, so the weight load and the gather issue together.
-// Synthesis epilogue: tap j stores (gr_j Re D_j, gi_j Im D_j) to its own
-// slot of the half-spectrum buffer F (an 8-byte record holds the slot:
-// plane P0 or P1 at the tap's bin, or an overflow slot for bins with more
-// than two taps, the gain gr and how gi follows from it); taps with zero
-// gain are skipped. No atomics: each slot has
+// adjoint); taps outside the window carry w = 0.
+// Synthesis epilogue (slot q RL + r = output t + T q + r OS): the tap stores
+// (gr Re D, gi Im D) to its own slot of the half-spectrum buffer F, from the
+// record {slot | mode << 30, gr} (plane P0 or P1 at the tap's bin, or an
+// overflow slot for bins with more than two taps; mode says how gi follows
+// from gr); taps with zero gain are skipped. No atomics: each slot has
 // exactly one writer, so the result is bitwise reproducible, and the
 // inverse column pass sums a bin's slots on load.
 // Reference semantics: radix.cu:46-114, radix_impl.cuh:27-42,100-143.
@@ -30,7 +35,7 @@
 namespace fcqt {
 
 constexpr int kBandThreads = 128;
-constexpr int kBandPoints = 16 * kBandThreads;  // complex values per task
+constexpr int kBandPoints = 16 * kBandThreads;  // complex values (and records) per task
 
 constexpr int band_lds(int M) { return (kBandPoints / M) * (M + M / 16 + 1); }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
@@ -53,119 +58,67 @@ __device__ __forceinline__ void store_coef(float* __restrict__ cre, float* __res
     }
 }
 
+// This thread's 16 records of its task (kernel order).
+__device__ __forceinline__ void load_records(int2* rv, const int2* __restrict__ rec, int task) {
+    const int2* rr = rec + (long)task * kBandPoints + threadIdx.x;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) rv[s] = rr[s * kBandThreads];
+}
+
+// Band inverse DFTs of one task, v already windowed; stores the
+// coefficients of the task's bands (units past the band count compute
+// padding that is never stored).
 template <int M, int LAYOUT>
-__device__ __forceinline__ void route_band(const int4 task, const int b, const float2* __restrict__ xs,
-                                           float* __restrict__ cre, float* __restrict__ cim,
-                                           const float* __restrict__ wt, const int4* __restrict__ bands,
-                                           const long ncoef, const float2* __restrict__ tws, float2* lds,
-                                           float2* tw2) {
+__device__ __forceinline__ void route_band(const int4 task, const int b, float2* v, float* __restrict__ cre,
+                                           float* __restrict__ cim, const long ncoef,
+                                           const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
     load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
-    Tw3<M> w3;
-    load_tw3<M>(w3, tws, threadIdx.x % P::T);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
-    const bool active = u < task.z;
-    const int4 bd = bands[task.w + (active ? u : 0)];   // {centre bin, r, l, side flag}
-    const float2* xb = xs + (long)b * kXStride;             // uniform bases, 32-bit offsets
-    const float* wu = wt + task.y;
-    const int ub = active ? u * M : 0;
-    // tap j < r reads bin c + j, tap j >= M - l reads bin c + j - M. Weights
-    // are exactly zero outside the window, so a dead tap only needs an
-    // in-bounds bin; units past the task's band count compute garbage that
-    // is never stored. Octave bands never leave (0, N/2) (checked when the
-    // tables are built); the DC and Nyquist side bands (flag bd.w) fold
-    // bins below 0 or above N/2 back with conjugation.
-    float2 v[16];
-    if (bd.w == 0) {
-        int kk[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int j = t + P::T * r;
-            kk[r] = min(max(bd.x + j - (j < bd.y ? 0 : M), 0), kL);
-        }
-        float w[16];
-        float2 xv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            w[r] = wu[ub + t + P::T * r];
-            xv[r] = xb[kk[r]];
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = make_float2(w[r] * xv[r].x, w[r] * xv[r].y);
-    } else {
-        int kk[16];
-        unsigned cj = 0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int j = t + P::T * r;
-            const int kp = bd.x + j - (j < bd.y ? 0 : M);
-            const bool neg = kp < 0, over = kp > kL;
-            kk[r] = min(max(neg ? -kp : (over ? kN - kp : kp), 0), kL);
-            cj |= (neg || over) ? 1u << r : 0u;
-        }
-        float w[16];
-        float2 xv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            w[r] = wu[ub + t + P::T * r];
-            xv[r] = xb[kk[r]];
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            v[r] = make_float2(w[r] * xv[r].x, (cj >> r) & 1u ? -w[r] * xv[r].y : w[r] * xv[r].y);
-    }
+    Tw3<M> w3;
+    load_tw3<M>(w3, tws, t);
     fft_unit<M, +1>(v, lds + u * P::US, t, tw2, w3);
-    if (active) {
-        const long ob = (long)b * ncoef + task.y;           // uniform
+    if (u < task.z) {
+        const long ob = (long)b * ncoef + task.y + u * M;   // uniform per unit
+        float* orow = cre + (LAYOUT == FCQT_PLANAR ? ob : 2 * ob);
+        float* oim = cim + (LAYOUT == FCQT_PLANAR ? ob : 0);
 #pragma unroll
         for (int q = 0; q < P::QL; ++q) {
 #pragma unroll
-            for (int r = 0; r < P::RL; ++r) {
-                const int m = ub + t + P::T * q + r * P::OS;
-                store_coef<LAYOUT>(cre + (LAYOUT == FCQT_PLANAR ? ob : 2 * ob),
-                                   cim + (LAYOUT == FCQT_PLANAR ? ob : 0), m, v[q * P::RL + r]);
-            }
+            for (int r = 0; r < P::RL; ++r)
+                store_coef<LAYOUT>(orow, oim, t + P::T * q + r * P::OS, v[q * P::RL + r]);
         }
     }
 }
 
 template <int M, int LAYOUT>
-__device__ __forceinline__ void scatter_band(const int4 task, const int b, const float* __restrict__ cre,
-                                             const float* __restrict__ cim, float* __restrict__ f,
-                                             const int2* __restrict__ scat, const long ncoef,
+__device__ __forceinline__ void scatter_band(const int4 task, const int b, const int2* rv,
+                                             const float* __restrict__ cre, const float* __restrict__ cim,
+                                             float* __restrict__ f, const long ncoef,
                                              const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
     load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
-    Tw3<M> w3;
-    load_tw3<M>(w3, tws, threadIdx.x % P::T);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
-    const int ub = active ? u * M : 0;
-    const long ib = (long)b * ncoef + task.y;               // uniform
+    Tw3<M> w3;
+    load_tw3<M>(w3, tws, t);
+    const long ib = (long)b * ncoef + task.y + (active ? u * M : 0);
     const float* cr = cre + (LAYOUT == FCQT_PLANAR ? ib : 2 * ib);
     const float* ci = cim + (LAYOUT == FCQT_PLANAR ? ib : 0);
     float2 v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, ub + t + P::T * r);
+    for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, t + P::T * r);
     fft_unit<M, -1>(v, lds + u * P::US, t, tw2, w3);
-    // records {slot | mode << 30, gain}: mode 0 gi = gr, 1 gi = -gr, 2 gi = 0;
-    // gain 0 = no slot. All 16 loads issue before the first store.
-    const int2* st = scat + task.y;                        // uniform
-    int2 rec[16];
-#pragma unroll
-    for (int q = 0; q < P::QL; ++q)
-#pragma unroll
-        for (int r = 0; r < P::RL; ++r) rec[q * P::RL + r] = st[ub + t + P::T * q + r * P::OS];
     if (active) {
         float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float gr = __int_as_float(rec[i].y);
+            const float gr = __int_as_float(rv[i].y);
             if (gr != 0.0f) {
-                const unsigned mode = (unsigned)rec[i].x >> 30;
-                const unsigned slot = min((unsigned)rec[i].x & 0x3fffffffu, (unsigned)(kFRow - 1));
+                const unsigned mode = (unsigned)rv[i].x >> 30;
+                const unsigned slot = min((unsigned)rv[i].x & 0x3fffffffu, (unsigned)(kFRow - 1));
                 const float gi = mode == 0 ? gr : (mode == 1 ? -gr : 0.0f);
                 fb[slot] = make_float2(gr * v[i].x, gi * v[i].y);
             }
@@ -183,23 +136,34 @@ template <int LAYOUT>
 __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __restrict__ xs,
                                                               float* __restrict__ cre,
                                                               float* __restrict__ cim,
-                                                              const float* __restrict__ wt,
-                                                              const int4* __restrict__ bands,
+                                                              const int2* __restrict__ rec,
                                                               const int4* __restrict__ tasks, int batch,
                                                               long ncoef, const float2* __restrict__ tws) {
     __shared__ float2 lds[kBandLds];
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
     decode_task(batch, task_id, b);
+    // records -> gathers -> window, before the task record is needed
+    int2 rv[16];
+    load_records(rv, rec, task_id);
+    const float2* xb = xs + (long)b * kXStride;
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float2 x = xb[min((unsigned)rv[r].x & 0x7fffffffu, (unsigned)kL)];
+        const float w = __int_as_float(rv[r].y);
+        const float im = __int_as_float(__float_as_int(w * x.y) ^ (rv[r].x & (int)0x80000000));
+        v[r] = make_float2(w * x.x, im);
+    }
     const int4 td = tasks[task_id];
     switch (td.x) {
-        case 32: route_band<32, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
-        case 64: route_band<64, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
-        case 128: route_band<128, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
-        case 256: route_band<256, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
-        case 512: route_band<512, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
-        case 1024: route_band<1024, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
-        case 2048: route_band<2048, LAYOUT>(td, b, xs, cre, cim, wt, bands, ncoef, tws, lds, tw2); break;
+        case 32: route_band<32, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
+        case 64: route_band<64, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
+        case 128: route_band<128, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
+        case 256: route_band<256, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
+        case 512: route_band<512, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
+        case 1024: route_band<1024, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
+        case 2048: route_band<2048, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
         default: break;
     }
 }
@@ -215,15 +179,17 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
     decode_task(batch, task_id, b);
+    int2 rv[16];
+    load_records(rv, scat, task_id);
     const int4 td = tasks[task_id];
     switch (td.x) {
-        case 32: scatter_band<32, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
-        case 64: scatter_band<64, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
-        case 128: scatter_band<128, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
-        case 256: scatter_band<256, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
-        case 512: scatter_band<512, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
-        case 1024: scatter_band<1024, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
-        case 2048: scatter_band<2048, LAYOUT>(td, b, cre, cim, f, scat, ncoef, tws, lds, tw2); break;
+        case 32: scatter_band<32, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
+        case 64: scatter_band<64, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
+        case 128: scatter_band<128, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
+        case 256: scatter_band<256, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
+        case 512: scatter_band<512, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
+        case 1024: scatter_band<1024, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
+        case 2048: scatter_band<2048, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
         default: break;
     }
 }
@@ -231,13 +197,11 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
 static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const float* cre, const float* cim,
                            int layout, int64_t batch) {
     if (!tab || !rec || !cre || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
-    if (!tab->tasks || !tab->bands || !tab->tw_stage || tab->ntasks < 1 || tab->nbands < 1 || tab->ncoef < 1)
-        return FCQT_EARG;
+    if (!tab->tasks || !tab->tw_stage || tab->ntasks < 1 || tab->ncoef < 1) return FCQT_EARG;
     if ((int64_t)tab->ntasks * batch >= (int64_t)1 << 31) return FCQT_EARG;
     if (layout != FCQT_PLANAR && layout != FCQT_INTERLEAVED) return FCQT_EARG;
     if (layout == FCQT_PLANAR && !cim) return FCQT_EARG;
-    if (!aligned(rec, 4) || !aligned(tab->tasks, 16) || !aligned(tab->bands, 16) || !aligned(tab->tw_stage, 16))
-        return FCQT_EALIGN;
+    if (!aligned(rec, 8) || !aligned(tab->tasks, 16) || !aligned(tab->tw_stage, 16)) return FCQT_EALIGN;
     if (layout == FCQT_PLANAR ? (!aligned(cre, 4) || !aligned(cim, 4)) : !aligned(cre, 8)) return FCQT_EALIGN;
     return FCQT_OK;
 }
@@ -246,24 +210,23 @@ static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const flo
 
 using namespace fcqt;
 
-extern "C" int fcqt_route_bands(const fcqt_tables* tab, const float* weights, const float* xs,
+extern "C" int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* xs,
                                 float* coef_re, float* coef_im, int layout, int64_t batch,
                                 hipStream_t stream) {
-    if (int e = check_band_args(tab, reinterpret_cast<const int32_t*>(weights), coef_re, coef_im, layout, batch))
-        return e;
+    if (int e = check_band_args(tab, route, coef_re, coef_im, layout, batch)) return e;
     if (!xs) return FCQT_EARG;
     if (!aligned(xs, 8)) return FCQT_EALIGN;
     const dim3 grid((unsigned)(tab->ntasks * batch));
     const auto* xx = reinterpret_cast<const float2*>(xs);
-    const auto* bb = reinterpret_cast<const int4*>(tab->bands);
+    const auto* rr = reinterpret_cast<const int2*>(route);
     const auto* tt = reinterpret_cast<const int4*>(tab->tasks);
     const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
     if (layout == FCQT_PLANAR)
         hipLaunchKernelGGL(k_route_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, xx, coef_re,
-                           coef_im, weights, bb, tt, (int)batch, (long)tab->ncoef, ws);
+                           coef_im, rr, tt, (int)batch, (long)tab->ncoef, ws);
     else
         hipLaunchKernelGGL(k_route_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream, xx,
-                           coef_re, coef_re, weights, bb, tt, (int)batch, (long)tab->ncoef, ws);
+                           coef_re, coef_re, rr, tt, (int)batch, (long)tab->ncoef, ws);
     return launch_status();
 }
 
@@ -272,7 +235,7 @@ extern "C" int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat, c
                                   hipStream_t stream) {
     if (int e = check_band_args(tab, scat, coef_re, coef_im, layout, batch)) return e;
     if (!f) return FCQT_EARG;
-    if (!aligned(f, 16) || !aligned(scat, 8)) return FCQT_EALIGN;
+    if (!aligned(f, 16)) return FCQT_EALIGN;
     const dim3 grid((unsigned)(tab->ntasks * batch));
     const auto* ss = reinterpret_cast<const int2*>(scat);
     const auto* tt = reinterpret_cast<const int4*>(tab->tasks);

@@ -12,7 +12,7 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 PLANAR = 0
 INTERLEAVED = 1
 
@@ -26,8 +26,7 @@ class Tables(ctypes.Structure):
     """Mirror of struct fcqt_tables."""
     _fields_ = [("tw_pass", ctypes.c_void_p), ("tw_half", ctypes.c_void_p),
                 ("tw_stage", ctypes.c_void_p), ("tasks", ctypes.c_void_p),
-                ("bands", ctypes.c_void_p), ("ntasks", ctypes.c_int32),
-                ("nbands", ctypes.c_int32), ("ncoef", ctypes.c_int64)]
+                ("ntasks", ctypes.c_int32), ("ncoef", ctypes.c_int64)]
 
 
 class NativeError(RuntimeError):

@@ -57,7 +57,7 @@ class FusedOctCQT:
         self.gspec = built["gspec"]
         self.ncoef = built["ncoef"]
         self.tables = {}
-        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks", "bands",
+        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks",
                      "tw_pass", "tw_half", "tw_stage"):
             self.tables[name] = torch.as_tensor(np.ascontiguousarray(built[name])).to(dev)
         # table bytes per direction (batch invariant, L2/MALL resident at batch)
@@ -65,8 +65,8 @@ class FusedOctCQT:
         tb = self.tables
         self._ct = _native.Tables(
             tw_pass=tb["tw_pass"].data_ptr(), tw_half=tb["tw_half"].data_ptr(),
-            tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(), bands=tb["bands"].data_ptr(),
-            ntasks=int(tb["tasks"].shape[0]), nbands=int(tb["bands"].shape[0]), ncoef=int(self.ncoef))
+            tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(),
+            ntasks=int(tb["tasks"].shape[0]), ncoef=int(self.ncoef))
         self._ws = {}
 
     # ------------------------------------------------------------ buffers

@@ -1,12 +1,16 @@
 """Host-side builder of the factored engine's tables (float64 -> fp32).
 
 Everything the kernels need that does not depend on the batch:
-  route    analysis weight per tap, fp32: window / M. The kernel gathers
+  route    analysis route records in the band kernels' order
+           [task][slot][thread] (kernel_taps): {bin | conj << 31, weight
+           bits}, the tap's gather bin and fp32 weight window / M
+           (route_taps: the weights in natural tap order). The kernel gathers
            the real FFT X (computed by the forward passes, untangle included)
            at the tap's bin, conjugated for taps past nn/2 (DC/Nyquist bands),
            multiplies by the weight and runs the band's unscaled inverse DFT.
            The band's 1/M is folded in (exact: M is a power of two).
-  route_b  synthesis-adjoint weight per tap: dual window times
+  route_b  synthesis-adjoint route records (route_b_taps: the weights): dual
+           window times
            (2/N)(1 - [k in {0, L}]/2) (the transpose of irfft is (2/N) rfft
            with bins 0 and L halved; the band's transpose of the forward DFT
            is the unscaled inverse DFT).
@@ -15,7 +19,8 @@ Everything the kernels need that does not depend on the batch:
            N - k with conjugation), the taps between lie outside the window.
            side = 1 marks the bands whose taps reach bin 0 or N/2 or beyond
            (DC, Nyquist); the others take the kernel's no-wrap path.
-  scat     synthesis record per tap, 2 x int32 {slot | mode << 30, gain}:
+  scat     synthesis record per tap, 2 x int32 {slot | mode << 30, gain},
+           in the band kernels' output order (scat_taps: natural tap order):
            the half spectrum is F[pos] = sum over taps of gdv DFT(C).
   scat_a   analysis-adjoint record {slot of idx | mode << 30, gr} with
            gr = g (N/2)/M (1 + edge), gi = -+gr (1 - edge): the transpose of
@@ -112,6 +117,38 @@ def band_tasks(gspec, points=POINTS_PER_TASK):
     return np.asarray(tasks, dtype=np.int32)
 
 
+def kernel_taps(tasks, out=False):
+    """Natural tap index of every (task, slot, thread) of the band kernels,
+    [ntasks, 16, 128] int64, -1 = padding (units past the task's bands).
+    Thread tid = u T + t (T = M / 16) works on unit (band) u. Inputs
+    (out=False): slot r holds tap t + T r. Outputs (out=True): slot q RL + r
+    holds output t + T q + r OS of the transform (the layout fft_unit leaves)."""
+    tasks = np.asarray(tasks)
+    res = np.full((tasks.shape[0], 16, 128), -1, dtype=np.int64)
+    slots = np.arange(16)
+    for ti, (M, off, nb, _) in enumerate(tasks.tolist()):
+        T = M // 16
+        tid = np.arange(128)
+        u, t = tid // T, tid % T
+        if not out:
+            j = t[None, :] + T * slots[:, None]
+        else:
+            R2 = 16 if M >= 256 else M // 16
+            RL = M // 256 if M > 256 else R2
+            j = t[None, :] + T * (slots // RL)[:, None] + (slots % RL)[:, None] * (M // RL)
+        res[ti] = np.where(u[None, :] < nb, off + u[None, :] * M + j, -1)
+    return res
+
+
+def _kernel_order(rec_taps, taps):
+    """[ncoef, 2] int32 per-tap records -> [ntasks * 16 * 128, 2] in kernel
+    order; padding slots get (0, 0) (weight or gain 0: no effect)."""
+    out = np.zeros(taps.shape + (2,), dtype=np.int32)
+    live = taps >= 0
+    out[live] = rec_taps[taps[live]]
+    return out.reshape(-1, 2)
+
+
 def band_descriptors(groups, nn=N):
     """{c, r, l, 0} per band, recovered from the group gather tables: the
     live taps j < r hold bins c..c+r-1 (c = the window centre) and the live
@@ -175,7 +212,12 @@ def build(groups, nn=N):
     bands = band_descriptors(groups)
     check_tasks(tasks, ncoef, bands)
     check_band_taps(bands, groups)
-    return dict(route=route, route_b=route_b, scat=scat, scat_a=scat_a, tasks=tasks, bands=bands,
+    tin, tout = kernel_taps(tasks), kernel_taps(tasks, out=True)
+    kbin = (k | (cf.astype(np.int64) << 31)).astype(np.uint32).view(np.int32)
+    route_rec = lambda w: _kernel_order(np.stack([kbin, _bits(w)], axis=1), tin)
+    return dict(route=route_rec(route), route_b=route_rec(route_b), route_taps=route, route_b_taps=route_b,
+                scat=_kernel_order(scat, tout), scat_a=_kernel_order(scat_a, tout),
+                scat_taps=scat, scat_a_taps=scat_a, tasks=tasks, bands=bands,
                 ovf_scat=ovf, ovf_scat_a=ovf_a,
                 tw_pass=pass_twiddles(), tw_half=half_twiddles(), tw_stage=stage_twiddles(),
                 gspec=gspec, ncoef=ncoef)

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 3
+#define FCQT_ABI_VERSION 4
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -63,10 +63,7 @@ typedef struct fcqt_tables {
     const float*   tw_half;   /* [32768] complex, W_65536^i */
     const float*   tw_stage;  /* [FCQT_TW_STAGE_LEN] complex band/pass stage twiddles */
     const int32_t* tasks;     /* [ntasks][4] band tasks: M, first coefficient, band count, first band */
-    const int32_t* bands;     /* [nbands][4] band descriptors: centre bin c, r, l, 0 (tap j < r reads
-                                 bin c+j, tap j >= M-l reads bin c+j-M, the others are zero) */
     int32_t        ntasks;
-    int32_t        nbands;
     int64_t        ncoef;     /* complex coefficients per slice (132992 for [3,4,2]/[8,16,32]) */
 } fcqt_tables;
 
@@ -90,18 +87,27 @@ const char* fcqt_last_hip_error(void);
 int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* xs, float* work,
                         int64_t batch, hipStream_t stream);
 
-/* Windowed band gathers + band inverse DFTs: coefficient m of band b is
+/* Band tables are in kernel order: for each task, 16 rows of 128 8-byte
+ * records (row s = slot s of each of the task's 128 threads), so a table has
+ * ntasks * 2048 records. Thread u T + t (T = M/16) works on unit u of the
+ * task (band u, units past the task's band count are padding with zero
+ * records); its input slot r is tap t + T r of that band, its output slot
+ * q RL + r is transform output t + T q + r OS (RL, OS: the last radix and
+ * its output stride). The host builder (flash_cqt/tables.py, kernel_taps)
+ * makes these tables from per-tap ones.
+ *
+ * Windowed band gathers + band inverse DFTs: coefficient m of band b is
  *   C_b[m] = sum_j w_j X~[k_j] e^{+2 pi i jm/M_b}
- * where k_j is the tap's bin from the band descriptor and X~ is X, or its
- * conjugate for taps past N/2 (folded to N - k). One fp32 weight per tap:
- * window/M gives the analysis, dual window * 2/N (halved at bins 0 and L)
- * the synthesis adjoint.
+ * where X~ is X, or its conjugate for taps past N/2 (folded to N - k). One
+ * record per tap {k | conj << 31, fp32 weight bits}: window/M gives the
+ * analysis, dual window * 2/N (halved at bins 0 and L) the synthesis
+ * adjoint; taps outside the window have weight 0.
  *   xs      [batch][FCQT_XSTRIDE] complex real-FFT spectrum (fcqt_packed_fft_fwd)
  *   coef    layout FCQT_PLANAR: coef_re, coef_im [batch][ncoef] fp32
  *           layout FCQT_INTERLEAVED: coef_re is [batch][ncoef] complex, coef_im unused
- *   weights [ncoef] fp32
+ *   route   [ntasks * 2048][2] int32 route records, kernel order
  * Replaces fwd_bands (radix.cu:46-62). */
-int fcqt_route_bands(const fcqt_tables* tab, const float* weights, const float* xs,
+int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, const float* xs,
                      float* coef_re, float* coef_im, int layout,
                      int64_t batch, hipStream_t stream);
 
@@ -120,7 +126,7 @@ int fcqt_route_bands(const fcqt_tables* tab, const float* weights, const float* 
  * analysis-adjoint table it is the analysis adjoint front half.
  *   f  [batch][FCQT_FROW] complex, 16-byte aligned
  * Replaces inv_bands (radix.cu:64-91) and adj_bands (radix.cu:93-114). */
-int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat /* [ncoef][2] */,
+int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat /* [ntasks * 2048][2], kernel order */,
                        const float* coef_re, const float* coef_im, int layout,
                        float* f, int64_t batch, hipStream_t stream);
 
@@ -140,7 +146,7 @@ int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float*
 
 /* Analysis in one call: fcqt_packed_fft_fwd then fcqt_route_bands.
  * xs is [batch][FCQT_XSTRIDE] and work [batch][32768] complex scratch. */
-int fcqt_analysis(const fcqt_tables* tab, const float* weights, const float* x,
+int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                   float* coef_re, float* coef_im, int layout,
                   float* xs, float* work, int64_t batch, hipStream_t stream);
 

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 3
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 4
 
 
 def test_status_strings(lib):
@@ -43,8 +43,8 @@ def test_status_strings(lib):
 
 def test_argument_errors_detected_before_any_launch(lib):
     from flash_cqt._native import Tables
-    tab = Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, bands=16, ntasks=1, nbands=1, ncoef=1)
-    bad = Tables(tw_pass=0, tw_half=0, tw_stage=0, tasks=0, bands=0, ntasks=0, nbands=0, ncoef=0)
+    tab = Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=1, ncoef=1)
+    bad = Tables(tw_pass=0, tw_half=0, tw_stage=0, tasks=0, ntasks=0, ncoef=0)
     s = ctypes.c_void_p(0)
     p = ctypes.c_void_p(4096)
     odd = ctypes.c_void_p(4100)

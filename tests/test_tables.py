@@ -55,10 +55,30 @@ def test_weights_and_band_descriptors(factored_tables, pkg_cqt_cpu):
     gd = np.concatenate([g[3].reshape(-1) for g in groups]).astype(np.float64)
     k = np.concatenate([g[0].reshape(-1) for g in groups])
     M = np.concatenate([np.full(g[0].size, g[0].shape[1]) for g in groups])
-    assert np.array_equal(t["route"].astype(np.float64) * M, gv)
+    assert np.array_equal(t["route_taps"].astype(np.float64) * M, gv)
     edge = (k == 0) | (k == N // 2)
-    assert np.array_equal(t["route_b"].astype(np.float64) * (N / 2.0) / (1 - 0.5 * edge), gd)
+    assert np.array_equal(t["route_b_taps"].astype(np.float64) * (N / 2.0) / (1 - 0.5 * edge), gd)
     T.check_band_taps(t["bands"], groups)
+    # kernel-order records: every (task, slot, thread) names its natural tap
+    # (gather bin, conjugation, weight / scatter record), padding is inert
+    cf = np.concatenate([g[4].reshape(-1) for g in groups]).astype(bool)
+    tin, tout = T.kernel_taps(t["tasks"]), T.kernel_taps(t["tasks"], out=True)
+    for taps in (tin, tout):
+        live = np.sort(taps[taps >= 0])
+        assert np.array_equal(live, np.arange(t["ncoef"]))        # a permutation of all taps
+    for name in ("route", "route_b"):
+        rec = t[name].reshape(tin.shape + (2,))
+        live = tin >= 0
+        word = rec[..., 0].view(np.uint32)
+        assert np.array_equal((word & 0x7FFFFFFF)[live], k[tin[live]])
+        assert np.array_equal((word >> 31)[live].astype(bool), cf[tin[live]])
+        assert np.array_equal(rec[..., 1].view(np.float32)[live], t[name + "_taps"][tin[live]])
+        assert not np.any(rec[~live])
+    for name in ("scat", "scat_a"):
+        rec = t[name].reshape(tout.shape + (2,))
+        live = tout >= 0
+        assert np.array_equal(rec[live], t[name + "_taps"][tout[live]])
+        assert not np.any(rec[~live])
 
 
 def test_schedule_sim_analysis_and_synthesis(factored_tables, oracle):
@@ -67,11 +87,11 @@ def test_schedule_sim_analysis_and_synthesis(factored_tables, oracle):
     x = x[:1].astype(np.float64)
     X = ks.packed_fft_fwd(x)
     assert snr_db(np.fft.rfft(x), X) > 140
-    C = ks.route_bands(X, t["route"], t["bands"], t["tasks"], t["ncoef"])
+    C = ks.route_bands(X, t["route_taps"], t["bands"], t["tasks"], t["ncoef"])
     obl, osd = oracle.fwd(x)
     Cref = oracle.flatten(obl, osd)
     assert snr_db(Cref, C) > 140
-    F = ks.scatter_bands(Cref, t["scat"], t["tasks"], t["ncoef"])
+    F = ks.scatter_bands(Cref, t["scat_taps"], t["tasks"], t["ncoef"])
     y = ks.packed_fft_inv(F, t["ovf_scat"])
     assert snr_db(oracle.bwd(obl, osd), y) > 140
 
@@ -80,12 +100,12 @@ def test_schedule_sim_adjoints(factored_tables, oracle):
     t = factored_tables
     rs = np.random.RandomState(12)
     G = rs.standard_normal((1, t["ncoef"])) + 1j * rs.standard_normal((1, t["ncoef"]))
-    F = ks.scatter_bands(G, t["scat_a"], t["tasks"], t["ncoef"])
+    F = ks.scatter_bands(G, t["scat_a_taps"], t["tasks"], t["ncoef"])
     gx = ks.packed_fft_inv(F, t["ovf_scat_a"])
     assert snr_db(oracle.fwd_adjoint(*oracle.unflatten(G)), gx) > 140
     u = rs.standard_normal((1, N))
     Xu = ks.packed_fft_fwd(u)
-    gC = ks.route_bands(Xu, t["route_b"], t["bands"], t["tasks"], t["ncoef"])
+    gC = ks.route_bands(Xu, t["route_b_taps"], t["bands"], t["tasks"], t["ncoef"])
     assert snr_db(oracle.flatten(*oracle.bwd_adjoint(u)), gC) > 140
 
 
@@ -103,7 +123,7 @@ def test_scatter_slots_unique_and_fold_lists(factored_tables):
     overflow slots exactly once, in the workgroup that owns its column."""
     from flash_cqt import tables as T
     for name in ("scat", "scat_a"):
-        rec = factored_tables[name]
+        rec = factored_tables[name + "_taps"]
         fold = factored_tables["ovf_" + name]
         live = rec[:, 1] != 0
         tgt = (rec[live, 0].view(np.uint32) & 0x3FFFFFFF).astype(np.int64)
