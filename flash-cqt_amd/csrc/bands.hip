@@ -42,6 +42,39 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 constexpr int kBandLds = cmax(cmax(cmax(band_lds(32), band_lds(64)), cmax(band_lds(128), band_lds(256))),
                               cmax(cmax(band_lds(512), band_lds(1024)), band_lds(2048)));
 
+// Coefficient addressing. FCQT_PLANAR / FCQT_INTERLEAVED: the engine layout
+// [batch][ncoef]. kSliced: the SlicedCQT block layout, interleaved complex:
+// batch = nsig * S slices (slice s of signal sig is batch row sig * S + s);
+// the coefficients of group g (first coefficient off_g, bins_g bands of
+// length M) form the block [nsig][bins_g][S * M] at batch * off_g, band i's
+// slice s at ((sig bins_g + i) S + s) M, and in octave groups (roll flag)
+// output m of the band transform sits at (m + M/4) mod M in even slices and
+// (m - M/4) mod M in odd slices (the SlicedCQT quarter roll; side groups are
+// [nsig][S][1][M] blocks, unrolled).
+constexpr int kSliced = 2;
+
+struct SliceMap {
+    const int4* __restrict__ groups;   // per task {off_g, bins_g, roll, 0}
+    int S;                             // slices per signal
+};
+
+template <int M, int LAYOUT>
+__device__ __forceinline__ void unit_coef(const int4 task, const int task_id, const int b, const int u,
+                                          const int batch, const long ncoef, const SliceMap& sm, long& base,
+                                          int& shift) {
+    if constexpr (LAYOUT == kSliced) {
+        const int4 g = sm.groups[task_id];
+        const int sig = b / sm.S;
+        const int s = b - sig * sm.S;
+        const int i = (task.y - g.x) / M + u;
+        base = (long)batch * g.x + ((long)(sig * g.y + i) * sm.S + s) * M;
+        shift = g.z ? ((s & 1) ? M - M / 4 : M / 4) : 0;
+    } else {
+        base = (long)b * ncoef + task.y + u * M;
+        shift = 0;
+    }
+}
+
 template <int LAYOUT>
 __device__ __forceinline__ float2 load_coef(const float* __restrict__ cre, const float* __restrict__ cim, int i) {
     if constexpr (LAYOUT == FCQT_PLANAR) return make_float2(cre[i], cim[i]);
@@ -69,8 +102,9 @@ __device__ __forceinline__ void load_records(int2* rv, const int2* __restrict__ 
 // coefficients of the task's bands (units past the band count compute
 // padding that is never stored).
 template <int M, int LAYOUT>
-__device__ __forceinline__ void route_band(const int4 task, const int b, float2* v, float* __restrict__ cre,
-                                           float* __restrict__ cim, const long ncoef,
+__device__ __forceinline__ void route_band(const int4 task, const int task_id, const int b, const int batch,
+                                           float2* v, float* __restrict__ cre, float* __restrict__ cim,
+                                           const long ncoef, const SliceMap sm,
                                            const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
     load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
@@ -80,22 +114,25 @@ __device__ __forceinline__ void route_band(const int4 task, const int b, float2*
     load_tw3<M>(w3, tws, t);
     fft_unit<M, +1>(v, lds + u * P::US, t, tw2, w3);
     if (u < task.z) {
-        const long ob = (long)b * ncoef + task.y + u * M;   // uniform per unit
+        long ob;
+        int shift;
+        unit_coef<M, LAYOUT>(task, task_id, b, u, batch, ncoef, sm, ob, shift);   // uniform per unit
         float* orow = cre + (LAYOUT == FCQT_PLANAR ? ob : 2 * ob);
         float* oim = cim + (LAYOUT == FCQT_PLANAR ? ob : 0);
 #pragma unroll
         for (int q = 0; q < P::QL; ++q) {
 #pragma unroll
             for (int r = 0; r < P::RL; ++r)
-                store_coef<LAYOUT>(orow, oim, t + P::T * q + r * P::OS, v[q * P::RL + r]);
+                store_coef<LAYOUT>(orow, oim, (t + P::T * q + r * P::OS + shift) & (M - 1), v[q * P::RL + r]);
         }
     }
 }
 
 template <int M, int LAYOUT>
-__device__ __forceinline__ void scatter_band(const int4 task, const int b, const int2* rv,
-                                             const float* __restrict__ cre, const float* __restrict__ cim,
-                                             float* __restrict__ f, const long ncoef,
+__device__ __forceinline__ void scatter_band(const int4 task, const int task_id, const int b, const int batch,
+                                             const int2* rv, const float* __restrict__ cre,
+                                             const float* __restrict__ cim, float* __restrict__ f,
+                                             const long ncoef, const SliceMap sm,
                                              const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
     load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
@@ -104,12 +141,14 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int b, const
     const bool active = u < task.z;
     Tw3<M> w3;
     load_tw3<M>(w3, tws, t);
-    const long ib = (long)b * ncoef + task.y + (active ? u * M : 0);
+    long ib;
+    int shift;
+    unit_coef<M, LAYOUT>(task, task_id, b, active ? u : 0, batch, ncoef, sm, ib, shift);
     const float* cr = cre + (LAYOUT == FCQT_PLANAR ? ib : 2 * ib);
     const float* ci = cim + (LAYOUT == FCQT_PLANAR ? ib : 0);
     float2 v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, t + P::T * r);
+    for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, (t + P::T * r + shift) & (M - 1));
     fft_unit<M, -1>(v, lds + u * P::US, t, tw2, w3);
     if (active) {
         float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
@@ -138,7 +177,8 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
                                                               float* __restrict__ cim,
                                                               const int2* __restrict__ rec,
                                                               const int4* __restrict__ tasks, int batch,
-                                                              long ncoef, const float2* __restrict__ tws) {
+                                                              long ncoef, const SliceMap sm,
+                                                              const float2* __restrict__ tws) {
     __shared__ float2 lds[kBandLds];
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
@@ -157,13 +197,13 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
     }
     const int4 td = tasks[task_id];
     switch (td.x) {
-        case 32: route_band<32, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
-        case 64: route_band<64, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
-        case 128: route_band<128, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
-        case 256: route_band<256, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
-        case 512: route_band<512, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
-        case 1024: route_band<1024, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
-        case 2048: route_band<2048, LAYOUT>(td, b, v, cre, cim, ncoef, tws, lds, tw2); break;
+        case 32: route_band<32, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
+        case 64: route_band<64, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
+        case 128: route_band<128, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
+        case 256: route_band<256, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
+        case 512: route_band<512, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
+        case 1024: route_band<1024, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
+        case 2048: route_band<2048, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
         default: break;
     }
 }
@@ -174,7 +214,8 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
                                                                 float* __restrict__ f,
                                                                 const int2* __restrict__ scat,
                                                                 const int4* __restrict__ tasks, int batch,
-                                                                long ncoef, const float2* __restrict__ tws) {
+                                                                long ncoef, const SliceMap sm,
+                                                                const float2* __restrict__ tws) {
     __shared__ float2 lds[kBandLds];
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
@@ -183,13 +224,13 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
     load_records(rv, scat, task_id);
     const int4 td = tasks[task_id];
     switch (td.x) {
-        case 32: scatter_band<32, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
-        case 64: scatter_band<64, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
-        case 128: scatter_band<128, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
-        case 256: scatter_band<256, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
-        case 512: scatter_band<512, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
-        case 1024: scatter_band<1024, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
-        case 2048: scatter_band<2048, LAYOUT>(td, b, rv, cre, cim, f, ncoef, tws, lds, tw2); break;
+        case 32: scatter_band<32, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
+        case 64: scatter_band<64, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
+        case 128: scatter_band<128, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
+        case 256: scatter_band<256, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
+        case 512: scatter_band<512, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
+        case 1024: scatter_band<1024, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
+        case 2048: scatter_band<2048, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
         default: break;
     }
 }
@@ -223,10 +264,10 @@ extern "C" int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, co
     const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
     if (layout == FCQT_PLANAR)
         hipLaunchKernelGGL(k_route_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, xx, coef_re,
-                           coef_im, rr, tt, (int)batch, (long)tab->ncoef, ws);
+                           coef_im, rr, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
     else
         hipLaunchKernelGGL(k_route_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream, xx,
-                           coef_re, coef_re, rr, tt, (int)batch, (long)tab->ncoef, ws);
+                           coef_re, coef_re, rr, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
     return launch_status();
 }
 
@@ -242,9 +283,42 @@ extern "C" int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat, c
     const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
     if (layout == FCQT_PLANAR)
         hipLaunchKernelGGL(k_scatter_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, coef_re,
-                           coef_im, f, ss, tt, (int)batch, (long)tab->ncoef, ws);
+                           coef_im, f, ss, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
     else
         hipLaunchKernelGGL(k_scatter_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream,
-                           coef_re, coef_re, f, ss, tt, (int)batch, (long)tab->ncoef, ws);
+                           coef_re, coef_re, f, ss, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
+    return launch_status();
+}
+
+extern "C" int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
+                                       const float* xs, float* coef, int64_t nsig, int64_t nslices,
+                                       hipStream_t stream) {
+    if (nsig < 1 || nslices < 1 || nsig > kMaxBatch || nslices > kMaxBatch) return FCQT_EARG;
+    const int64_t batch = nsig * nslices;
+    if (int e = check_band_args(tab, route, coef, coef, FCQT_INTERLEAVED, batch)) return e;
+    if (!xs || !groups) return FCQT_EARG;
+    if (!aligned(xs, 8) || !aligned(groups, 16)) return FCQT_EALIGN;
+    const dim3 grid((unsigned)(tab->ntasks * batch));
+    hipLaunchKernelGGL(k_route_bands<kSliced>, grid, dim3(kBandThreads), 0, stream,
+                       reinterpret_cast<const float2*>(xs), coef, coef, reinterpret_cast<const int2*>(route),
+                       reinterpret_cast<const int4*>(tab->tasks), (int)batch, (long)tab->ncoef,
+                       SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices},
+                       reinterpret_cast<const float2*>(tab->tw_stage));
+    return launch_status();
+}
+
+extern "C" int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
+                                         const float* coef, float* f, int64_t nsig, int64_t nslices,
+                                         hipStream_t stream) {
+    if (nsig < 1 || nslices < 1 || nsig > kMaxBatch || nslices > kMaxBatch) return FCQT_EARG;
+    const int64_t batch = nsig * nslices;
+    if (int e = check_band_args(tab, scat, coef, coef, FCQT_INTERLEAVED, batch)) return e;
+    if (!f || !groups) return FCQT_EARG;
+    if (!aligned(f, 16) || !aligned(groups, 16)) return FCQT_EALIGN;
+    const dim3 grid((unsigned)(tab->ntasks * batch));
+    hipLaunchKernelGGL(k_scatter_bands<kSliced>, grid, dim3(kBandThreads), 0, stream, coef, coef, f,
+                       reinterpret_cast<const int2*>(scat), reinterpret_cast<const int4*>(tab->tasks),
+                       (int)batch, (long)tab->ncoef, SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices},
+                       reinterpret_cast<const float2*>(tab->tw_stage));
     return launch_status();
 }

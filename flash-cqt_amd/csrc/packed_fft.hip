@@ -47,9 +47,39 @@ __device__ __forceinline__ float2 dense_bin(const float2* __restrict__ fb, int i
     return cadd(fb[i], fb[kFStride + i]);
 }
 
+// SlicedCQT framing read by the sliced column pass: batch row sig * S + s is
+// slice s of signal sig, sample j = x[sig][2H (s - 1) + jj] win[jj] with
+// jj = (j + H) mod N in even slices and (j - H) mod N in odd slices
+// (H = N/4; samples outside the signal are zero). This is the zero padding,
+// 50%-overlap unfold, Tukey window and quarter roll of the reference
+// SlicedCQT._slice in one read.
+struct SliceSrc {
+    const float* sig;   // [nsig][len]
+    const float* win;   // [N]
+    long len;
+    int S;
+};
+
+constexpr int kQuarter = kN / 4;
+
+__device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const float* xrow, long s0, int sh, int n) {
+    const int jj = (2 * n + sh) & (kN - 1);       // even: the pair (jj, jj + 1) stays inside the slice
+    const long i = s0 + jj;
+    const long i0 = min(max(i, 0l), src.len - 1), i1 = min(max(i + 1, 0l), src.len - 1);
+    const float a = xrow[i0] * ((i >= 0 && i < src.len) ? 1.0f : 0.0f);
+    const float c = xrow[i1] * ((i + 1 >= 0 && i + 1 < src.len) ? 1.0f : 0.0f);
+    // rounded products (the empty asm keeps them out of the first butterfly's
+    // fused multiply-adds): bitwise the windowed slice the reference framing
+    // builds before its transform
+    float p0 = src.win[jj] * a, p1 = src.win[jj + 1] * c;
+    asm volatile("" : "+v"(p0), "+v"(p1));
+    return make_float2(p0, p1);
+}
+
+template <bool SLICED>
 __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, float2* __restrict__ out,
                                                  const float2* __restrict__ twp,
-                                                 const float2* __restrict__ tws) {
+                                                 const float2* __restrict__ tws, const SliceSrc src) {
     using P = Plan<128>;
     __shared__ float2 lds[kColsPerWg * P::US];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -59,9 +89,19 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
     const int t = threadIdx.x >> 4;                // thread within the column FFT, < 8
     const int n2 = cg * kColsPerWg + c;
     float2 v[16];
-    const float2* xb = in + (long)b * kL;
+    if constexpr (SLICED) {
+        const int sig = b / src.S;
+        const int sl = b - sig * src.S;
+        const float* xrow = src.sig + (long)sig * src.len;
+        const long s0 = 2l * kQuarter * (sl - 1);
+        const int sh = (sl & 1) ? kN - kQuarter : kQuarter;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
+        for (int r = 0; r < 16; ++r) v[r] = sliced_pair(src, xrow, s0, sh, 256 * (t + 8 * r) + n2);
+    } else {
+        const float2* xb = in + (long)b * kL;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
+    }
     // every twiddle this thread needs, in flight with the data
     __shared__ float2 tw2[tw2_len<128>()];
     load_tw2_lds<128>(tw2, tws, threadIdx.x, 128);
@@ -300,9 +340,9 @@ extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float
         !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
         return FCQT_EALIGN;
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
-    hipLaunchKernelGGL(k_col_fwd, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
+    hipLaunchKernelGGL(k_col_fwd<false>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
                        reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
-                       reinterpret_cast<const float2*>(tab->tw_pass), tws);
+                       reinterpret_cast<const float2*>(tab->tw_pass), tws, SliceSrc{nullptr, nullptr, 1, 1});
     if (int e = launch_status()) return e;
     hipLaunchKernelGGL(k_row_fwd, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
                        reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(xs),
@@ -325,5 +365,61 @@ extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, c
     if (int e = launch_status()) return e;
     hipLaunchKernelGGL(k_row_inv, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
                        reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(y), tws);
+    return launch_status();
+}
+
+extern "C" int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int64_t sig_len, const float* window,
+                                  int64_t nsig, int64_t nslices, float* xs, float* work, hipStream_t stream) {
+    if (!tab || !sig || !window || !xs || !work || sig_len < 1 || nsig < 1 || nslices < 1) return FCQT_EARG;
+    if (nsig > kMaxBatch || nslices > kMaxBatch || nsig * nslices > kMaxBatch) return FCQT_EARG;
+    if (!tab->tw_pass || !tab->tw_half || !tab->tw_stage) return FCQT_EARG;
+    if (!aligned(sig, 4) || !aligned(window, 4) || !aligned(xs, 8) || !aligned(work, 8) ||
+        !aligned(tab->tw_pass, 8) || !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
+        return FCQT_EALIGN;
+    const int64_t batch = nsig * nslices;
+    const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
+    hipLaunchKernelGGL(k_col_fwd<true>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
+                       nullptr, reinterpret_cast<float2*>(work), reinterpret_cast<const float2*>(tab->tw_pass), tws,
+                       SliceSrc{sig, window, (long)sig_len, (int)nslices});
+    if (int e = launch_status()) return e;
+    hipLaunchKernelGGL(k_row_fwd, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
+                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(xs),
+                       reinterpret_cast<const float2*>(tab->tw_half), tws);
+    return launch_status();
+}
+
+namespace fcqt {
+// Overlap-add of rolled slices: out[sig][p] = sum over the (at most two)
+// slices s with 0 <= q - 2H s < N, q = p + 2H, of y[sig S + s][jj],
+// jj = (q - 2H s - H) mod N in even slices and (q - 2H s + H) mod N in odd
+// ones (the reference's roll by +-H, overlap-add and 2H trim).
+__global__ __launch_bounds__(256) void k_overlap_add(const float* __restrict__ y, float* __restrict__ out, int S,
+                                                     long length) {
+    const long p = (long)blockIdx.x * 256 + threadIdx.x;
+    const int sig = blockIdx.y;
+    if (p >= length) return;
+    const long q = p + 2 * kQuarter;
+    const long sh = q / (2 * kQuarter);
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const long s = sh - 1 + k;
+        if (s >= 0 && s < S) {
+            const int j = (int)(q - 2 * kQuarter * s);
+            const int jj = (j + ((s & 1) ? kQuarter : kN - kQuarter)) & (kN - 1);
+            acc += y[((long)sig * S + s) * kN + jj];
+        }
+    }
+    out[(long)sig * length + p] = acc;
+}
+}  // namespace fcqt
+
+extern "C" int fcqt_overlap_add(const float* y, float* out, int64_t nsig, int64_t nslices, int64_t length,
+                                hipStream_t stream) {
+    if (!y || !out || nsig < 1 || nslices < 1 || length < 1 || nsig > 65535) return FCQT_EARG;
+    if (nsig * nslices > kMaxBatch || length > nslices * 2 * (int64_t)kQuarter) return FCQT_EARG;
+    if (!aligned(y, 4) || !aligned(out, 4)) return FCQT_EALIGN;
+    const dim3 grid((unsigned)((length + 255) / 256), (unsigned)nsig);
+    hipLaunchKernelGGL(k_overlap_add, grid, dim3(256), 0, stream, y, out, (int)nslices, (long)length);
     return launch_status();
 }

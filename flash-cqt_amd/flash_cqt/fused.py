@@ -53,11 +53,11 @@ class FusedOctCQT:
         self.cqt = cqt
         self.lib = _native.load()
 
-        built = T.build(_np_groups(cqt))
+        built = T.build(_np_groups(cqt), noct=len(cqt.groups))
         self.gspec = built["gspec"]
         self.ncoef = built["ncoef"]
         self.tables = {}
-        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks",
+        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks", "slice_groups",
                      "tw_pass", "tw_half", "tw_stage"):
             self.tables[name] = torch.as_tensor(np.ascontiguousarray(built[name])).to(dev)
         # table bytes per direction (batch invariant, L2/MALL resident at batch)
@@ -175,6 +175,49 @@ class FusedOctCQT:
                                               _native.ptr(c_im), layout, _native.ptr(w[self._FBUF[table]]),
                                               _native.ptr(w["W"]), _native.ptr(y), B,
                                               _native.stream_handle()), "synthesis")
+
+    # ------------------------------------------- SlicedCQT framing
+
+    def slice_fft(self, sig, window, nslices, xs, work):
+        """X of every 65536-sample slice of the signals sig [nsig, len]
+        (SlicedCQT framing: zero pad, 50% overlap, window, quarter roll)."""
+        if sig.dim() != 2 or sig.shape[1] < 1:
+            raise ValueError("sig must be [nsig, len]")
+        nsig, length = sig.shape
+        self._need(sig, nsig * length * 4, "sig")
+        self._need(window, N * 4, "window")
+        B = nsig * nslices
+        self._need(xs, B * T.XSTRIDE * 8, "xs")
+        self._need(work, B * L * 8, "work")
+        _native.check(self.lib.fcqt_slice_fft_fwd(self._ct, _native.ptr(sig), length, _native.ptr(window), nsig,
+                                                  nslices, _native.ptr(xs), _native.ptr(work),
+                                                  _native.stream_handle()), "slice_fft_fwd")
+
+    def route_bands_sliced(self, xs, coef, nsig, nslices, table="route"):
+        """Coefficients of every slice into the SlicedCQT block layout
+        (complex64, nsig * nslices * ncoef values)."""
+        B = nsig * nslices
+        self._need(xs, B * T.XSTRIDE * 8, "xs")
+        self._need(coef, B * self.ncoef * 8, "coef")
+        _native.check(self.lib.fcqt_route_bands_sliced(self._ct, _native.ptr(self.tables[table]),
+                                                       _native.ptr(self.tables["slice_groups"]), _native.ptr(xs),
+                                                       _native.ptr(coef), nsig, nslices,
+                                                       _native.stream_handle()), "route_bands_sliced")
+
+    def scatter_bands_sliced(self, coef, f, nsig, nslices, table="scat"):
+        B = nsig * nslices
+        self._need(coef, B * self.ncoef * 8, "coef")
+        self._need(f, B * T.FROW * 8, "f")
+        _native.check(self.lib.fcqt_scatter_bands_sliced(self._ct, _native.ptr(self.tables[table]),
+                                                         _native.ptr(self.tables["slice_groups"]),
+                                                         _native.ptr(coef), _native.ptr(f), nsig, nslices,
+                                                         _native.stream_handle()), "scatter_bands_sliced")
+
+    def overlap_add(self, y, out, nsig, nslices, length):
+        self._need(y, nsig * nslices * N * 4, "y")
+        self._need(out, nsig * length * 4, "out")
+        _native.check(self.lib.fcqt_overlap_add(_native.ptr(y), _native.ptr(out), nsig, nslices, length,
+                                                _native.stream_handle()), "overlap_add")
 
     # ------------------------------------------------- reference surface
 

@@ -12,6 +12,14 @@ and bwd(blocks, side) -> x. engine="auto" uses the fused HIP engine
 (TrainableCQT, differentiable) on a GPU device with sl_len 65536 and the
 pure-torch OctCQT otherwise; "hip" forces the fused engine, "torch" the
 pure-torch one. Assigning self.cqt swaps engines as in the reference.
+
+With the HIP engine and no gradient to record, fwd and bwd run the framing
+inside the engine's kernels (fcqt_slice_fft_fwd, fcqt_route_bands_sliced,
+fcqt_scatter_bands_sliced, fcqt_overlap_add): slices are read straight from
+the signal, coefficients are written and read in the block layout with the
+quarter roll applied, and the inverse slices are rolled and overlap-added
+in one pass. Blocks returned by that path are views of one buffer; passing
+them back to bwd reads that buffer without a copy.
 """
 import math
 
@@ -121,11 +129,86 @@ class SlicedCQT:
             out.append(torch.where(even, torch.roll(c, sgn * r, -1), torch.roll(c, -sgn * r, -1)))
         return out
 
+    # ------------------------------------------- fused framing (HIP engine)
+
+    def _fused(self, *tensors):
+        """The HIP engine when the framing can run inside it: engine is
+        TrainableCQT, inputs on its GPU, and no gradient is being recorded."""
+        f = getattr(self.cqt, "f", None)
+        if type(self.cqt).__name__ != "TrainableCQT" or f is None:
+            return None
+        ts = [t for t in tensors if t is not None]
+        if any(t.device != f.dev for t in ts):
+            return None
+        if torch.is_grad_enabled() and any(t.requires_grad for t in ts):
+            return None
+        return f
+
+    def _ws(self, f, nsig, S):
+        key = (nsig, S)
+        ws = getattr(self, "_fused_ws", None)
+        if ws is None or ws[0] != key:
+            from . import tables as T
+            B = nsig * S
+            dev = f.dev
+            ws = (key, dict(X=torch.empty(B, T.XSTRIDE, 2, device=dev), W=torch.empty(B, T.L, 2, device=dev),
+                            F=torch.zeros(B, T.FROW, 2, device=dev), Y=torch.empty(B, self.sl_len, device=dev)))
+            self._fused_ws = ws
+        return ws[1]
+
+    def _fwd_fused(self, f, x):
+        B, C, L = x.shape
+        S = self._num_slices(L)
+        nsig = B * C
+        sig = x.reshape(nsig, L).to(torch.float32).contiguous()
+        ws = self._ws(f, nsig, S)
+        f.slice_fft(sig, self.tw.to(torch.float32).contiguous(), S, ws["X"], ws["W"])
+        coef = torch.empty(nsig * S * f.ncoef, dtype=torch.complex64, device=f.dev)
+        f.route_bands_sliced(ws["X"], coef, nsig, S)
+        ng = len(self.oct_bins)
+        blocks, side = [], []
+        for gi, (b, M, off) in enumerate(f.gspec):
+            v = coef[nsig * S * off:nsig * S * (off + b * M)]
+            if gi < ng:
+                blocks.append(v.view(B, C, b, S * M))
+            else:
+                side.append(v.view(B, C, S, b, M))
+        return blocks, side
+
+    def _block_buffer(self, f, blocks, side, nsig, S):
+        """One complex64 buffer in the fused block layout: the blocks' own
+        storage when they are the views _fwd_fused returned, else a copy."""
+        parts = list(blocks) + (list(side) if side is not None else [])
+        if side is not None and all(p.dtype == torch.complex64 and p.is_contiguous() for p in parts):
+            base = parts[0].data_ptr()
+            if all(p.data_ptr() == base + 8 * nsig * S * off for p, (_, _, off) in zip(parts, f.gspec)):
+                return torch.as_strided(parts[0], (nsig * S * f.ncoef,), (1,))
+        coef = torch.zeros(nsig * S * f.ncoef, dtype=torch.complex64, device=f.dev)
+        for p, (b, M, off) in zip(parts, f.gspec):
+            coef[nsig * S * off:nsig * S * (off + b * M)] = p.reshape(-1).to(torch.complex64)
+        return coef
+
+    def _bwd_fused(self, f, blocks, side, length):
+        B, C = blocks[0].shape[:2]
+        S = blocks[0].shape[-1] // self.size_per_oct[0]
+        nsig = B * C
+        coef = self._block_buffer(f, blocks, side, nsig, S)
+        ws = self._ws(f, nsig, S)
+        f.scatter_bands_sliced(coef, ws["F"], nsig, S)
+        f.packed_ifft(ws["F"], ws["Y"], ws["W"])
+        n = S * 2 * self.H if length is None else min(int(length), S * 2 * self.H)
+        out = torch.empty(B, C, n, dtype=torch.float32, device=f.dev)
+        f.overlap_add(ws["Y"], out, nsig, S, n)
+        return out
+
     # --------------------------------------------------- whole buffer api
 
     def fwd(self, x):
         """x [B, C, L] -> (blocks, side): blocks[i] [B, C, oct_bins[i], S*size_per_oct[i]]
         in time order along the last axis, side (dc, nyq) per slice [B, C, S, 1, M]."""
+        f = self._fused(x)
+        if f is not None:
+            return self._fwd_fused(f, x)
         B, C, _ = x.shape
         sl = self._slice(x)
         S = sl.shape[2]
@@ -137,6 +220,9 @@ class SlicedCQT:
 
     def bwd(self, blocks, side=None, length=None):
         """Inverse of fwd; length trims the tail padding."""
+        f = self._fused(*blocks, *(side if side is not None else []))
+        if f is not None:
+            return self._bwd_fused(f, blocks, side, length)
         B, C = blocks[0].shape[:2]
         S = blocks[0].shape[-1] // self.size_per_oct[0]
         blocks = [c.reshape(B, C, b, S, m).permute(0, 1, 3, 2, 4)

@@ -40,6 +40,8 @@ Everything the kernels need that does not depend on the batch:
            entry = bin | overflow index << 16, -1 = none.
   tasks    band tasks {M, first coefficient, band count, first band}:
            consecutive bands of one group, at most POINTS / M per task.
+  slice_groups  per task {off_g, bins_g, roll, 0} of its group, for the
+           SlicedCQT block layout (see fcqt_route_bands_sliced).
   tw_pass  W_L^(k1 n2) at k1*256 + n2 (column pass of the packed FFT).
   tw_half  W_N^i, i < L (retangle of the inverse).
   tw_stage Stockham stage twiddles W_{NS R}^(r k) in [r][k] rows for
@@ -172,12 +174,29 @@ def band_descriptors(groups, nn=N):
     return np.asarray(rows, dtype=np.int32)
 
 
-def build(groups, nn=N):
+def slice_groups(tasks, gspec, noct):
+    """Per task {off_g, bins_g, roll, 0} of the task's group (first
+    coefficient, band count, 1 for the noct octave groups whose SlicedCQT
+    blocks are quarter-rolled, 0 for the side groups)."""
+    out = []
+    for M, first, _, _ in np.asarray(tasks).tolist():
+        for gi, (b, Mg, off) in enumerate(gspec):
+            if off <= first < off + b * Mg:
+                assert Mg == M and (first - off) % M == 0
+                out.append([off, b, 1 if gi < noct else 0, 0])
+                break
+        else:
+            raise AssertionError("task outside every group")
+    return np.asarray(out, dtype=np.int32)
+
+
+def build(groups, nn=N, noct=None):
     """Tables for the fused engine from OctCQT group tables.
 
     groups: list of numpy (idx, gv, pos, gdv, conj) in coefficient order
     (octave groups, then DC, then Nyquist), as OctCQT.np_groups +
-    np_side_groups. Returns a dict of numpy arrays.
+    np_side_groups; noct: number of octave groups (default: all but the two
+    side groups). Returns a dict of numpy arrays.
     """
     assert nn == N, "the fused engine is built for 65536-sample slices"
     gspec, off = [], 0
@@ -218,6 +237,7 @@ def build(groups, nn=N):
     return dict(route=route_rec(route), route_b=route_rec(route_b), route_taps=route, route_b_taps=route_b,
                 scat=_kernel_order(scat, tout), scat_a=_kernel_order(scat_a, tout),
                 scat_taps=scat, scat_a_taps=scat_a, tasks=tasks, bands=bands,
+                slice_groups=slice_groups(tasks, gspec, len(groups) - 2 if noct is None else noct),
                 ovf_scat=ovf, ovf_scat_a=ovf_a,
                 tw_pass=pass_twiddles(), tw_half=half_twiddles(), tw_stage=stage_twiddles(),
                 gspec=gspec, ncoef=ncoef)

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 4
+#define FCQT_ABI_VERSION 5
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -155,6 +155,48 @@ int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
 int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* ovf,
                    const float* coef_re, const float* coef_im, int layout,
                    float* f, float* work, float* y, int64_t batch, hipStream_t stream);
+
+/* ---- SlicedCQT framing fused into the engine (same kernels, other I/O) ----
+ * nsig signals of sig_len samples, each cut into nslices 65536-sample slices
+ * at hop N/2 (batch row sig * nslices + s); H = N/4.
+ *
+ * Sliced real FFT: slice s of signal sig is x[sig][2H (s - 1) + jj] * window[jj]
+ * with jj = (j + H) mod N for even s and (j - H) mod N for odd s (zero
+ * outside the signal): the zero padding, 50%-overlap unfold, Tukey window
+ * and quarter roll, read straight from the signal by the column pass.
+ *   sig    [nsig][sig_len] fp32,  window [65536] fp32
+ *   xs, work as for fcqt_packed_fft_fwd with batch nsig * nslices
+ * Replaces SlicedCQT._slice (sliced.py:106-117) + the pack copy and fft3. */
+int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int64_t sig_len, const float* window,
+                       int64_t nsig, int64_t nslices, float* xs, float* work, hipStream_t stream);
+
+/* Route + band IDFTs storing straight into the SlicedCQT block layout
+ * (interleaved complex, nsig * nslices * ncoef values): group g (first
+ * coefficient off_g, bins_g bands of length M, per-task table `groups`
+ * [ntasks][4] = {off_g, bins_g, roll, 0}) is the block [nsig][bins_g][nslices * M]
+ * at nsig * nslices * off_g; in octave groups (roll = 1) band output m of an
+ * even slice goes to (m + M/4) mod M, of an odd slice to (m - M/4) mod M;
+ * side groups are [nsig][nslices][1][M] blocks.
+ * Replaces fwd_bands + SlicedCQT._arrange(fwd) and the block permute of
+ * SlicedCQT.fwd (sliced.py:119-131, 134-146). */
+int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
+                            const float* xs, float* coef, int64_t nsig, int64_t nslices,
+                            hipStream_t stream);
+
+/* Band DFTs + slot scatter reading the same block layout (the inverse
+ * arrange). F rules as fcqt_scatter_bands, batch nsig * nslices.
+ * Replaces the block permute + SlicedCQT._arrange(bwd) of SlicedCQT.bwd and
+ * inv_bands (sliced.py:148-157). */
+int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
+                              const float* coef, float* f, int64_t nsig, int64_t nslices,
+                              hipStream_t stream);
+
+/* Overlap-add of the inverse slices (y [nsig * nslices][65536], the output of
+ * fcqt_packed_fft_inv): out[sig][p], p < length <= nslices * 2H, sums the
+ * slices covering p + 2H after rolling even slices by +H and odd by -H.
+ * Replaces the roll, overlap-add and trim of SlicedCQT.bwd (sliced.py:158-166). */
+int fcqt_overlap_add(const float* y, float* out, int64_t nsig, int64_t nslices, int64_t length,
+                     hipStream_t stream);
 
 /* Zero n floats with a fill kernel (graph-capture safe, no hipMemsetAsync). */
 int fcqt_fill_zero(float* buf, int64_t n, hipStream_t stream);

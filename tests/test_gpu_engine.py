@@ -320,6 +320,31 @@ def test_sliced_stream_equals_whole_buffer():
     assert md < 1e-5 and rd < 1e-5
 
 
+def test_sliced_fused_framing_equals_engine_composition():
+    """The fused framing (slices read from the signal, block-layout stores,
+    overlap-add kernel) is bitwise the engine + torch-glue composition that
+    autograd uses, forward and inverse, and the glue path still carries
+    gradients."""
+    from flash_cqt import SlicedCQT
+    s = SlicedCQT(device=_dev())
+    x = gpu(sliced_input()[:, :, :99999])       # odd length: unaligned signal rows
+    with torch.no_grad():
+        bl, sd = s.fwd(x)                      # fused
+        y = s.bwd(bl, sd, length=x.shape[-1])
+    xg = x.clone().requires_grad_(True)
+    bl2, sd2 = s.fwd(xg)                       # engine + glue (autograd)
+    for a, b in zip(bl + sd, bl2 + sd2):
+        assert a.shape == b.shape and torch.equal(a, b.detach())
+    y2 = s.bwd(bl2, sd2, length=x.shape[-1])
+    assert torch.equal(y, y2.detach())
+    (y2 * x).sum().backward()
+    assert xg.grad is not None and torch.isfinite(xg.grad).all()
+    with torch.no_grad():                      # separate blocks (not views of one buffer) and no side
+        y3 = s.bwd([c.clone() for c in bl], None, length=x.shape[-1])
+    y4 = s.bwd([c.detach().clone().requires_grad_(True) for c in bl2], None, length=x.shape[-1])
+    assert torch.equal(y3, y4.detach())
+
+
 def test_sliced_config5_round_trip():
     """Config 5: B=8, 441000 samples, exponential sweep 43 Hz -> 20 kHz over
     10 s plus N(0, 0.1^2) noise, 15 slices per signal."""
