@@ -12,14 +12,16 @@ are measured the same way (median of event-timed replays) and reported in
   - the hipFFT-call baseline: the package's pure-torch OctCQT (torch.fft ->
     hipFFT/rocFFT) on the GPU, graph-captured, same inputs;
   - the host-core baseline: the oracle's torch port of the reference
-    OctCQT on the box's CPU cores, a bounded sample (cpu_baseline).
+    OctCQT on the box's CPU cores, a bounded sample (cpu_baseline);
+  - the SlicedCQT streaming workload in "sliced".
 Per-kernel launch durations are timed with hipEvents on the launch stream
 (graphs of back-to-back launches); "roofline" reports the dominant kernel's
 algorithmic bytes per launch over its duration against 8 TB/s.
 
 Extra modes (for rocprofv3 counter runs): --kernels-only runs a few
 launches of every kernel plus a plain copy of known size (the calibration
-kernel for FETCH_SIZE / WRITE_SIZE) and prints nothing else.
+kernel for FETCH_SIZE / WRITE_SIZE) and prints nothing else; --sliced-only
+runs the SlicedCQT workload alone and prints its JSON object.
 """
 import argparse
 import json
@@ -77,6 +79,17 @@ def snr_db(ref, got):
     e = ref.square().sum()
     d = (ref - got.double()).square().sum()
     return float("inf") if float(d) == 0 else float(10 * torch.log10(e / d))
+
+
+def json_safe(v):
+    """Strict JSON: an infinite SNR (bitwise-equal results) becomes the string "inf"."""
+    if isinstance(v, dict):
+        return {k: json_safe(u) for k, u in v.items()}
+    if isinstance(v, (list, tuple)):
+        return [json_safe(u) for u in v]
+    if isinstance(v, float) and not math.isfinite(v):
+        return str(v)
+    return v
 
 
 def capture(fn):
@@ -140,6 +153,42 @@ def torch_fft_baseline(cqt_gpu, x):
         if ok:
             return median_ms(g.replay), "hipGraph", eager
         return median_ms(fn), "eager", eager
+
+
+def sliced_workload(dev):
+    """SlicedCQT, batch 8 x 441000 samples (10 s chirp 43 Hz..20 kHz
+    + N(0, 0.1^2)), 65536-sample slices at 50% overlap, fwd + bwd. Timed
+    graph-replayed with the framing inside the engine's kernels, and beside it
+    the same round trip composed of the host framing ops around the same
+    engine (the reference's structure)."""
+    from flash_cqt import SlicedCQT
+    T, n = 10.0, np.arange(441000) / FS
+    k = math.log(20000.0 / 43.0)
+    sweep = np.sin(2 * np.pi * 43.0 * T / k * (np.exp(n / T * k) - 1.0))
+    rs = np.random.RandomState(0)
+    x = torch.as_tensor((sweep[None, None, :] + 0.1 * rs.standard_normal((8, 1, n.size)))
+                        .astype(np.float32)).to(dev)
+    s = SlicedCQT(fs=FS, device=dev)
+    fused = lambda: s.bwd(*s.fwd(x), length=x.shape[-1])
+    res = {"workload": "configs[4] SlicedCQT batch 8 x 441000 samples, 50% overlap",
+           "slices": 8 * s._num_slices(x.shape[-1]), "samples": 8 * x.shape[-1]}
+    with torch.no_grad():
+        y = fused().clone()
+        res["roundtrip_snr_db"] = snr_db(x, y)
+        g, out = capture(fused)
+        res["replay_vs_eager_db"] = replay_matches_eager(g, out, y, [out])
+        ms = median_ms(g.replay)
+        s._fused = lambda *a: None            # the host-framing composition
+        yc = fused().clone()
+        gc, _ = capture(fused)
+        msc = median_ms(gc.replay)
+        del s._fused
+    res.update({"ms": ms, "msamples_per_s": res["samples"] / (ms * 1e-3) / 1e6,
+                "host_framing_ms": msc, "speedup_vs_host_framing": msc / ms,
+                "host_framing_vs_fused_db": snr_db(yc, y)})
+    log(f"sliced: {ms:.4f} ms  {res['msamples_per_s']:.0f} Msamples/s  rt {res['roundtrip_snr_db']:.1f} dB"
+        f"  (host framing {msc:.4f} ms)")
+    return res
 
 
 def cpu_baseline(budget_s=12.0, max_reps=400):
@@ -266,6 +315,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-lib-baseline", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
+    ap.add_argument("--sliced-only", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -282,6 +332,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.sliced_only:
+        print(json.dumps(json_safe(sliced_workload(dev))), flush=True)
+        return
     cqt_gpu = OctCQT([3, 4, 2], [8, 16, 32], fs=FS, audio_len=N, device=dev)
     f = FusedOctCQT(cqt_gpu, dev)
     if args.kernels_only:
@@ -352,6 +405,7 @@ def main():
             "alg_bytes_per_launch": kern[dom]["alg_bytes_per_call"],
             "ms_per_launch": kern[dom]["ms_per_launch"], "batch": B}
 
+    sliced = sliced_workload(dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
     line = {
@@ -367,11 +421,12 @@ def main():
         "hbm_gbps": gbps, "hbm_frac": gbps / PEAK_GBPS, "wall_s_timed": wall,
         "per_batch": {str(k): v for k, v in per_batch.items()},
         "kernels": kern,
+        "sliced": sliced,
         "table_bytes": f.table_bytes,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(json_safe(line)), flush=True)
 
 
 if __name__ == "__main__":
