@@ -98,20 +98,33 @@ __device__ __forceinline__ void load_records(int2* rv, const int2* __restrict__ 
     for (int s = 0; s < 16; ++s) rv[s] = rr[s * kBandThreads];
 }
 
-// Band inverse DFTs of one task, v already windowed; stores the
-// coefficients of the task's bands (units past the band count compute
-// padding that is never stored).
+// Route + band inverse DFTs of one task; stores the coefficients of the
+// task's bands (units past the band count compute padding that is never
+// stored). The twiddle loads issue before the gathers, so their latency
+// hides under the record and gather round trips.
 template <int M, int LAYOUT>
 __device__ __forceinline__ void route_band(const int4 task, const int task_id, const int b, const int batch,
-                                           float2* v, float* __restrict__ cre, float* __restrict__ cim,
+                                           const int2* rv, const float2* __restrict__ xb,
+                                           float* __restrict__ cre, float* __restrict__ cim,
                                            const long ncoef, const SliceMap sm,
                                            const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
-    load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
+    Tw2Copy<M, kBandThreads> c2;
+    fetch_tw2<M, kBandThreads>(c2, tws, threadIdx.x);
     Tw3<M> w3;
     load_tw3<M>(w3, tws, t);
+    // v = w X[k], conjugated for taps past Nyquist
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float2 x = xb[min((unsigned)rv[r].x & 0x7fffffffu, (unsigned)kL)];
+        const float w = __int_as_float(rv[r].y);
+        const float im = __int_as_float(__float_as_int(w * x.y) ^ (rv[r].x & (int)0x80000000));
+        v[r] = make_float2(w * x.x, im);
+    }
+    put_tw2<M, kBandThreads>(tw2, c2, threadIdx.x);
     fft_unit<M, +1>(v, lds + u * P::US, t, tw2, w3);
     if (u < task.z) {
         long ob;
@@ -130,17 +143,16 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
 
 template <int M, int LAYOUT>
 __device__ __forceinline__ void scatter_band(const int4 task, const int task_id, const int b, const int batch,
-                                             const int2* rv, const float* __restrict__ cre,
+                                             const int2* __restrict__ scat, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
                                              const long ncoef, const SliceMap sm,
                                              const float2* __restrict__ tws, float2* lds, float2* tw2) {
     using P = Plan<M>;
-    load_tw2_lds<M>(tw2, tws, threadIdx.x, kBandThreads);
     const int u = threadIdx.x / P::T;
     const int t = threadIdx.x - u * P::T;
     const bool active = u < task.z;
-    Tw3<M> w3;
-    load_tw3<M>(w3, tws, t);
+    // coefficients first, then the twiddles, then the records (needed only
+    // after the transform)
     long ib;
     int shift;
     unit_coef<M, LAYOUT>(task, task_id, b, active ? u : 0, batch, ncoef, sm, ib, shift);
@@ -149,6 +161,13 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, (t + P::T * r + shift) & (M - 1));
+    Tw2Copy<M, kBandThreads> c2;
+    fetch_tw2<M, kBandThreads>(c2, tws, threadIdx.x);
+    Tw3<M> w3;
+    load_tw3<M>(w3, tws, t);
+    int2 rv[16];
+    load_records(rv, scat, task_id);
+    put_tw2<M, kBandThreads>(tw2, c2, threadIdx.x);
     fft_unit<M, -1>(v, lds + u * P::US, t, tw2, w3);
     if (active) {
         float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
@@ -183,29 +202,24 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
     decode_task(batch, task_id, b);
-    // records -> gathers -> window, before the task record is needed
+    // the records issue first (they need the task index only); the task
+    // record then selects the band length, and the gathers follow inside
     int2 rv[16];
     load_records(rv, rec, task_id);
     const float2* xb = xs + (long)b * kXStride;
-    float2 v[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const float2 x = xb[min((unsigned)rv[r].x & 0x7fffffffu, (unsigned)kL)];
-        const float w = __int_as_float(rv[r].y);
-        const float im = __int_as_float(__float_as_int(w * x.y) ^ (rv[r].x & (int)0x80000000));
-        v[r] = make_float2(w * x.x, im);
-    }
     const int4 td = tasks[task_id];
+#define FCQT_ROUTE(M_) route_band<M_, LAYOUT>(td, task_id, b, batch, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
-        case 32: route_band<32, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
-        case 64: route_band<64, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
-        case 128: route_band<128, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
-        case 256: route_band<256, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
-        case 512: route_band<512, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
-        case 1024: route_band<1024, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
-        case 2048: route_band<2048, LAYOUT>(td, task_id, b, batch, v, cre, cim, ncoef, sm, tws, lds, tw2); break;
+        case 32: FCQT_ROUTE(32); break;
+        case 64: FCQT_ROUTE(64); break;
+        case 128: FCQT_ROUTE(128); break;
+        case 256: FCQT_ROUTE(256); break;
+        case 512: FCQT_ROUTE(512); break;
+        case 1024: FCQT_ROUTE(1024); break;
+        case 2048: FCQT_ROUTE(2048); break;
         default: break;
     }
+#undef FCQT_ROUTE
 }
 
 template <int LAYOUT>
@@ -220,19 +234,19 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
     decode_task(batch, task_id, b);
-    int2 rv[16];
-    load_records(rv, scat, task_id);
     const int4 td = tasks[task_id];
+#define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT>(td, task_id, b, batch, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
-        case 32: scatter_band<32, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
-        case 64: scatter_band<64, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
-        case 128: scatter_band<128, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
-        case 256: scatter_band<256, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
-        case 512: scatter_band<512, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
-        case 1024: scatter_band<1024, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
-        case 2048: scatter_band<2048, LAYOUT>(td, task_id, b, batch, rv, cre, cim, f, ncoef, sm, tws, lds, tw2); break;
+        case 32: FCQT_SCATTER(32); break;
+        case 64: FCQT_SCATTER(64); break;
+        case 128: FCQT_SCATTER(128); break;
+        case 256: FCQT_SCATTER(256); break;
+        case 512: FCQT_SCATTER(512); break;
+        case 1024: FCQT_SCATTER(1024); break;
+        case 2048: FCQT_SCATTER(2048); break;
         default: break;
     }
+#undef FCQT_SCATTER
 }
 
 static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const float* cre, const float* cim,

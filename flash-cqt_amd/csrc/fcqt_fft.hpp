@@ -211,6 +211,33 @@ __device__ __forceinline__ void load_tw2_lds(float2* tl, const float2* __restric
     for (int i = tid; i < N4; i += nthreads) dst[i] = src[i];
 }
 
+// The same copy in two halves, for a workgroup of NT threads: fetch_tw2
+// issues the loads into registers (early, so that their latency hides under
+// the data loads), put_tw2 writes them to LDS before the first barrier.
+template <int M, int NT>
+struct Tw2Copy {
+    static constexpr int N4 = tw2_len<M>() / 2;
+    static constexpr int PER = (N4 + NT - 1) / NT;
+    float4 d[PER];
+};
+
+template <int M, int NT>
+__device__ __forceinline__ void fetch_tw2(Tw2Copy<M, NT>& c, const float2* __restrict__ tws, int tid) {
+    constexpr int N4 = Tw2Copy<M, NT>::N4;
+    const float4* src = reinterpret_cast<const float4*>(tws + tw_off(16, Plan<M>::R2));
+#pragma unroll
+    for (int k = 0; k < Tw2Copy<M, NT>::PER; ++k) c.d[k] = src[min(tid + k * NT, N4 - 1)];
+}
+
+template <int M, int NT>
+__device__ __forceinline__ void put_tw2(float2* tl, const Tw2Copy<M, NT>& c, int tid) {
+    constexpr int N4 = Tw2Copy<M, NT>::N4;
+    float4* dst = reinterpret_cast<float4*>(tl);
+#pragma unroll
+    for (int k = 0; k < Tw2Copy<M, NT>::PER; ++k)
+        if (tid + k * NT < N4) dst[tid + k * NT] = c.d[k];
+}
+
 // Third-stage bases W^k, W^2k, W^4k (k = j mod 256) of each of a thread's
 // 16 / R3 butterflies, loaded with the unit's data so that no table read
 // waits behind the transform's barriers.
