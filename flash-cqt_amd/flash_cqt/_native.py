@@ -91,8 +91,17 @@ def ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
-def stream_handle():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_handle(device_index=None):
+    """hipStream_t (as an int) of the current torch stream of a device
+    (default: the current device)."""
+    if device_index is None:
+        device_index = torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(device_index)
+    return torch.cuda.current_stream(device_index).cuda_stream
 
 
 def require_device(t, name, dtype=torch.float32):

@@ -67,7 +67,9 @@ class FusedOctCQT:
             tw_pass=tb["tw_pass"].data_ptr(), tw_half=tb["tw_half"].data_ptr(),
             tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(),
             ntasks=int(tb["tasks"].shape[0]), ncoef=int(self.ncoef))
+        self._tp = {k: v.data_ptr() for k, v in tb.items()}
         self._ws = {}
+        self._wp = {}
 
     # ------------------------------------------------------------ buffers
 
@@ -81,13 +83,14 @@ class FusedOctCQT:
                 z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
                 self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=z(B, T.FROW, 2), FA=z(B, T.FROW, 2),
                                    KR=z(B, self.ncoef), KI=z(B, self.ncoef), XO=z(B, N))
+            self._wp[B] = {k: v.data_ptr() for k, v in self._ws[B].items()}
         return self._ws[B]
 
     _FBUF = {"scat": "F", "scat_a": "FA"}
 
     def _check_x(self, x):
-        if x.dim() != 2 or x.shape[1] != N:
-            raise ValueError(f"x must be [B, {N}], got {tuple(x.shape)}")
+        if x.dim() != 2 or x.shape[1] != N or x.shape[0] < 1:
+            raise ValueError(f"x must be [B, {N}] with B >= 1, got {tuple(x.shape)}")
         _native.require_device(x, "x")
         if x.device != self.dev:
             raise ValueError(f"x is on {x.device}, engine on {self.dev}")
@@ -129,7 +132,7 @@ class FusedOctCQT:
         self._need(xs, B * T.XSTRIDE * 8, "xs")
         self._need(work, B * L * 8, "work")
         _native.check(self.lib.fcqt_packed_fft_fwd(self._ct, _native.ptr(x), _native.ptr(xs),
-                                                   _native.ptr(work), B, _native.stream_handle()),
+                                                   _native.ptr(work), B, _native.stream_handle(self.dev.index)),
                       "packed_fft_fwd")
 
     def route_bands(self, xs, out_re, out_im, layout, table="route"):
@@ -137,14 +140,14 @@ class FusedOctCQT:
         self._need_coef(out_re, out_im, layout, B, "out")
         _native.check(self.lib.fcqt_route_bands(self._ct, _native.ptr(self.tables[table]), _native.ptr(xs),
                                                 _native.ptr(out_re), _native.ptr(out_im), layout, B,
-                                                _native.stream_handle()), "route_bands")
+                                                _native.stream_handle(self.dev.index)), "route_bands")
 
     def scatter_bands(self, c_re, c_im, layout, f, table="scat"):
         B = self._batch(f, T.FROW * 8, "f")
         self._need_coef(c_re, c_im, layout, B, "coef")
         _native.check(self.lib.fcqt_scatter_bands(self._ct, _native.ptr(self.tables[table]), _native.ptr(c_re),
                                                   _native.ptr(c_im), layout, _native.ptr(f), B,
-                                                  _native.stream_handle()), "scatter_bands")
+                                                  _native.stream_handle(self.dev.index)), "scatter_bands")
 
     def packed_ifft(self, f, y, work, table="scat"):
         """y = irfft of the half spectrum held in f's slots (filled with `table`)."""
@@ -153,7 +156,7 @@ class FusedOctCQT:
         self._need(work, B * L * 8, "work")
         _native.check(self.lib.fcqt_packed_fft_inv(self._ct, _native.ptr(self.tables["ovf_" + table]),
                                                    _native.ptr(f), _native.ptr(y), _native.ptr(work),
-                                                   B, _native.stream_handle()), "packed_fft_inv")
+                                                   B, _native.stream_handle(self.dev.index)), "packed_fft_inv")
 
     def analysis(self, x, out_re, out_im, layout, table="route"):
         """x [B, N] -> coefficients (planar planes or one interleaved buffer)."""
@@ -163,7 +166,7 @@ class FusedOctCQT:
         _native.check(self.lib.fcqt_analysis(self._ct, _native.ptr(self.tables[table]), _native.ptr(x),
                                              _native.ptr(out_re), _native.ptr(out_im), layout,
                                              _native.ptr(w["X"]), _native.ptr(w["W"]), B,
-                                             _native.stream_handle()), "analysis")
+                                             _native.stream_handle(self.dev.index)), "analysis")
 
     def synthesis(self, c_re, c_im, layout, y, table="scat"):
         """coefficients -> y [B, N] (table 'scat' synthesis, 'scat_a' analysis adjoint)."""
@@ -174,7 +177,7 @@ class FusedOctCQT:
                                               _native.ptr(self.tables["ovf_" + table]), _native.ptr(c_re),
                                               _native.ptr(c_im), layout, _native.ptr(w[self._FBUF[table]]),
                                               _native.ptr(w["W"]), _native.ptr(y), B,
-                                              _native.stream_handle()), "synthesis")
+                                              _native.stream_handle(self.dev.index)), "synthesis")
 
     # ------------------------------------------- SlicedCQT framing
 
@@ -191,7 +194,7 @@ class FusedOctCQT:
         self._need(work, B * L * 8, "work")
         _native.check(self.lib.fcqt_slice_fft_fwd(self._ct, _native.ptr(sig), length, _native.ptr(window), nsig,
                                                   nslices, _native.ptr(xs), _native.ptr(work),
-                                                  _native.stream_handle()), "slice_fft_fwd")
+                                                  _native.stream_handle(self.dev.index)), "slice_fft_fwd")
 
     def route_bands_sliced(self, xs, coef, nsig, nslices, table="route"):
         """Coefficients of every slice into the SlicedCQT block layout
@@ -202,7 +205,7 @@ class FusedOctCQT:
         _native.check(self.lib.fcqt_route_bands_sliced(self._ct, _native.ptr(self.tables[table]),
                                                        _native.ptr(self.tables["slice_groups"]), _native.ptr(xs),
                                                        _native.ptr(coef), nsig, nslices,
-                                                       _native.stream_handle()), "route_bands_sliced")
+                                                       _native.stream_handle(self.dev.index)), "route_bands_sliced")
 
     def scatter_bands_sliced(self, coef, f, nsig, nslices, table="scat"):
         B = nsig * nslices
@@ -211,32 +214,46 @@ class FusedOctCQT:
         _native.check(self.lib.fcqt_scatter_bands_sliced(self._ct, _native.ptr(self.tables[table]),
                                                          _native.ptr(self.tables["slice_groups"]),
                                                          _native.ptr(coef), _native.ptr(f), nsig, nslices,
-                                                         _native.stream_handle()), "scatter_bands_sliced")
+                                                         _native.stream_handle(self.dev.index)), "scatter_bands_sliced")
 
     def overlap_add(self, y, out, nsig, nslices, length):
         self._need(y, nsig * nslices * N * 4, "y")
         self._need(out, nsig * length * 4, "out")
         _native.check(self.lib.fcqt_overlap_add(_native.ptr(y), _native.ptr(out), nsig, nslices, length,
-                                                _native.stream_handle()), "overlap_add")
+                                                _native.stream_handle(self.dev.index)), "overlap_add")
 
     # ------------------------------------------------- reference surface
+
+    # fwd/bwd check only the caller's tensors: the workspace buffers and
+    # tables are the engine's own, sized at allocation, so their pointers are
+    # cached per batch size and passed as they are (host cost per call is
+    # then about that of the kernel launches themselves).
 
     def fwd(self, x):
         """x [B, 65536] fp32 -> (KR, KI) [B, ncoef], workspace views."""
         self._check_x(x)
-        w = self._workspace(x.shape[0])
-        self.analysis(x, w["KR"], w["KI"], _native.PLANAR)
+        B = x.shape[0]
+        w = self._workspace(B)
+        p = self._wp[B]
+        _native.check(self.lib.fcqt_analysis(self._ct, self._tp["route"], x.data_ptr(), p["KR"], p["KI"],
+                                             _native.PLANAR, p["X"], p["W"], B,
+                                             _native.stream_handle(self.dev.index)), "analysis")
         return w["KR"], w["KI"]
 
     def bwd(self, KR, KI):
         """(KR, KI) [B, ncoef] -> XO [B, 65536], a workspace view."""
-        B = KR.shape[0]
-        if KR.shape != (B, self.ncoef) or KI.shape != (B, self.ncoef):
+        B = KR.shape[0] if KR.dim() else 0
+        if B < 1 or KR.shape != (B, self.ncoef) or KI.shape != (B, self.ncoef):
             raise ValueError(f"KR, KI must be [B, {self.ncoef}]")
         _native.require_device(KR, "KR")
         _native.require_device(KI, "KI")
+        if KR.device != self.dev or KI.device != self.dev:
+            raise ValueError(f"KR, KI must be on {self.dev}")
         w = self._workspace(B)
-        self.synthesis(KR, KI, _native.PLANAR, w["XO"])
+        p = self._wp[B]
+        _native.check(self.lib.fcqt_synthesis(self._ct, self._tp["scat"], self._tp["ovf_scat"], KR.data_ptr(),
+                                              KI.data_ptr(), _native.PLANAR, p["F"], p["W"], p["XO"], B,
+                                              _native.stream_handle(self.dev.index)), "synthesis")
         return w["XO"]
 
     def blocks_view(self, KR, KI):

@@ -402,3 +402,10 @@ def test_bad_inputs_rejected(fused):
         fused.fwd(torch.zeros(2, N))
     with pytest.raises(ValueError):
         fused.bwd(torch.zeros(2, 5, device=_dev()), torch.zeros(2, 5, device=_dev()))
+    with pytest.raises(ValueError):
+        fused.fwd(torch.zeros(0, N, device=_dev()))
+    with pytest.raises(ValueError):                              # non-contiguous coefficients
+        kr = torch.zeros(fused.ncoef, 2, device=_dev()).t()
+        fused.bwd(kr, kr)
+    with pytest.raises(ValueError):                              # wrong dtype
+        fused.fwd(torch.zeros(1, N, device=_dev(), dtype=torch.float64))
