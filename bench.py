@@ -15,7 +15,8 @@ configs[2]); batch 1 (configs[1], sinusoids + noise) and batch 16 are in
     hipFFT/rocFFT) on the GPU, graph-captured, same inputs;
   - the host-core baseline: the oracle's torch port of the reference
     OctCQT on the box's CPU cores, a bounded sample (cpu_baseline);
-  - the SlicedCQT streaming workload in "sliced".
+  - the SlicedCQT streaming workload (configs[4]) in "sliced";
+  - the TrainableCQT differentiable step in "training_step".
 Per-kernel launch durations are timed with hipEvents on the launch stream
 (graphs of back-to-back launches); "roofline" reports the dominant kernel's
 algorithmic bytes per launch over its duration against 8 TB/s.
@@ -218,6 +219,35 @@ def sliced_workload(dev):
                 "host_framing_vs_fused_db": snr_db(yc, y)})
     log(f"sliced: {ms:.4f} ms  {res['msamples_per_s']:.0f} Msamples/s  rt {res['roundtrip_snr_db']:.1f} dB"
         f"  (host framing {msc:.4f} ms)")
+    return res
+
+
+def training_step(dev, cqt_gpu):
+    """TrainableCQT differentiable step at batch 16 (analysis ->
+    synthesis -> MSE against a second randn target -> backward), stream
+    launches with autograd, beside the same step through the pure-torch
+    OctCQT (torch.fft -> hipFFT/rocFFT) with autograd."""
+    from flash_cqt.trainable import TrainableCQT
+    train = TrainableCQT(cqt_gpu, dev)
+    x, tgt = randn(16, 0).to(dev), randn(16, 1).to(dev)
+    xg = x.clone().requires_grad_(True)
+
+    def step_with(engine):
+        def step():
+            xg.grad = None
+            y = engine.bwd(*engine.fwd(xg))
+            ((y - tgt) ** 2).mean().backward()
+        return step
+
+    ours, ref = step_with(train), step_with(cqt_gpu)
+    ref()
+    g_ref = xg.grad.clone()
+    ours()
+    res = {"workload": "configs[3] TrainableCQT step, batch 16: fwd -> bwd -> MSE -> backward",
+           "grad_snr_db_vs_torch_fft": snr_db(g_ref, xg.grad)}
+    ms, ms_ref = per_step_ms(ours, steps=30), per_step_ms(ref, steps=10)
+    res.update({"ms": ms, "steps_per_s": 1e3 / ms, "hipfft_baseline_ms": ms_ref, "speedup_vs_hipfft": ms_ref / ms})
+    log(f"training step B=16: {ms:.4f} ms  (hipFFT autograd {ms_ref:.4f} ms)  grad {res['grad_snr_db_vs_torch_fft']:.1f} dB")
     return res
 
 
@@ -438,6 +468,7 @@ def main():
             "ms_per_launch": kern[dom]["ms_per_launch"], "batch": B}
 
     sliced = sliced_workload(dev)
+    train = training_step(dev, cqt_gpu)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
     line = {
@@ -455,6 +486,7 @@ def main():
         "per_batch": {str(k): v for k, v in per_batch.items()},
         "kernels": kern,
         "sliced": sliced,
+        "training_step": train,
         "table_bytes": f.table_bytes,
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -11,7 +11,9 @@ transpose is the packed FFT plus the route engine with the dual-window
 record (flash_cqt/tables.py). Nothing is saved for backward.
 
 Coefficients live in one interleaved complex64 buffer [B, ncoef]; the
-returned blocks are views into it (no per-group copies).
+returned blocks are views into it (no per-group copies), and bwd reads that
+buffer in place when it is handed the same views back (the reference
+concatenates the blocks, trainable.py:161-164).
 """
 import torch
 
@@ -31,26 +33,45 @@ class TrainableCQT:
         self.ngroups = len(cqt.groups)
 
     # ------------------------------------------------ engine directions
+    # The inputs reaching these are [B, N] float32 or [B, ncoef] complex64,
+    # contiguous and on the engine's device (fwd/bwd and the autograd
+    # Functions make them so); outputs are fresh buffers of the right size.
+    # So the launches go straight to the C ABI with the engine's cached
+    # workspace and table pointers.
 
-    def _analysis(self, x):
-        kc = torch.empty(x.shape[0], self.ncoef, dtype=torch.complex64, device=self.dev)
-        self.f.analysis(x, kc, None, _native.INTERLEAVED, table="route")
+    def _launch_analysis(self, x, table):
+        B = x.shape[0]
+        f = self.f
+        f._workspace(B)
+        p = f._wp[B]
+        kc = torch.empty(B, self.ncoef, dtype=torch.complex64, device=self.dev)
+        _native.check(f.lib.fcqt_analysis(f._ct, f._tp[table], x.data_ptr(), kc.data_ptr(), None,
+                                          _native.INTERLEAVED, p["X"], p["W"], B,
+                                          _native.stream_handle(self.dev.index)), "analysis")
         return kc
 
-    def _synthesis(self, kc):
-        y = torch.empty(kc.shape[0], N, dtype=torch.float32, device=self.dev)
-        self.f.synthesis(kc, None, _native.INTERLEAVED, y, table="scat")
+    def _launch_synthesis(self, kc, table, fbuf):
+        B = kc.shape[0]
+        f = self.f
+        f._workspace(B)
+        p = f._wp[B]
+        y = torch.empty(B, N, dtype=torch.float32, device=self.dev)
+        _native.check(f.lib.fcqt_synthesis(f._ct, f._tp[table], f._tp["ovf_" + table], kc.data_ptr(), None,
+                                           _native.INTERLEAVED, p[fbuf], p["W"], y.data_ptr(), B,
+                                           _native.stream_handle(self.dev.index)), "synthesis")
         return y
 
+    def _analysis(self, x):
+        return self._launch_analysis(x, "route")
+
+    def _synthesis(self, kc):
+        return self._launch_synthesis(kc, "scat", "F")
+
     def _adj_analysis(self, gk):
-        gx = torch.empty(gk.shape[0], N, dtype=torch.float32, device=self.dev)
-        self.f.synthesis(gk, None, _native.INTERLEAVED, gx, table="scat_a")
-        return gx
+        return self._launch_synthesis(gk, "scat_a", "FA")
 
     def _adj_synthesis(self, gy):
-        gk = torch.empty(gy.shape[0], self.ncoef, dtype=torch.complex64, device=self.dev)
-        self.f.analysis(gy, gk, None, _native.INTERLEAVED, table="route_b")
-        return gk
+        return self._launch_analysis(gy, "route_b")
 
     # ---------------------------------------------------- public surface
 
@@ -60,9 +81,28 @@ class TrainableCQT:
         xf = x.reshape(-1, N)
         if xf.dtype != torch.float32:
             xf = xf.float()
+        if xf.device != self.dev:
+            raise ValueError(f"x is on {xf.device}, engine on {self.dev}")
+        if xf.shape[0] < 1:
+            raise ValueError("x needs at least one slice")
         kc = _Analysis.apply(xf.contiguous(), self)
-        views = [kc[:, off:off + b * M].view(*lead, b, M) for b, M, off in self.gspec]
+        views = [c.view(*lead, b, M) for c, (b, M, _) in
+                 zip(kc.split([b * M for b, M, _ in self.gspec], dim=1), self.gspec)]
         return views[:self.ngroups], views[self.ngroups:]
+
+    def _base_of(self, parts, B):
+        """The [B, ncoef] complex64 buffer whose consecutive group views the
+        parts are (as fwd returns them), else None."""
+        base = parts[0]._base
+        if base is None or base.device != self.dev or base.dtype != torch.complex64 \
+                or base.shape != (B, self.ncoef) or not base.is_contiguous():
+            return None
+        ptr = base.data_ptr()
+        for c, (b, M, off) in zip(parts, self.gspec):
+            if c._base is not base or c.data_ptr() != ptr + 8 * off or c.stride()[-2:] != (M, 1) \
+                    or c.shape[-2:] != (b, M):
+                return None
+        return base
 
     def bwd(self, blocks, side=None):
         """Inverse of fwd; side=None treats the DC and Nyquist bands as zero."""
@@ -70,6 +110,10 @@ class TrainableCQT:
         B = 1
         for d in lead:
             B *= d
+        if side is not None and B >= 1:
+            flat = self._base_of(list(blocks) + list(side), B)
+            if flat is not None:
+                return _Synthesis.apply(flat, self).reshape(*lead, N)
         parts = [c.reshape(B, -1) for c in list(blocks)]
         if side is not None:
             parts += [c.reshape(B, -1) for c in list(side)]
@@ -79,6 +123,8 @@ class TrainableCQT:
         flat = torch.cat([p.to(torch.complex64) for p in parts], dim=-1)
         if flat.shape[-1] != self.ncoef:
             raise ValueError(f"blocks carry {flat.shape[-1]} coefficients, expected {self.ncoef}")
+        if flat.device != self.dev:
+            raise ValueError(f"blocks are on {flat.device}, engine on {self.dev}")
         return _Synthesis.apply(flat.contiguous(), self).reshape(*lead, N)
 
 
