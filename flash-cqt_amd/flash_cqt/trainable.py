@@ -86,8 +86,9 @@ class TrainableCQT:
         if xf.shape[0] < 1:
             raise ValueError("x needs at least one slice")
         kc = _Analysis.apply(xf.contiguous(), self)
-        views = [c.view(*lead, b, M) for c, (b, M, _) in
-                 zip(kc.split([b * M for b, M, _ in self.gspec], dim=1), self.gspec)]
+        # one narrow per group (not a multi-output split): the blocks stay
+        # single views, which autograd lets a caller modify in place
+        views = [kc.narrow(1, off, b * M).view(*lead, b, M) for b, M, off in self.gspec]
         return views[:self.ngroups], views[self.ngroups:]
 
     def _base_of(self, parts, B):

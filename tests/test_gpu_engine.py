@@ -260,6 +260,28 @@ def test_training_step_gradient_config4(train, oracle):
     assert db >= 120
 
 
+def test_trainable_in_place_views_and_coefficient_loss(train):
+    """bwd of fwd's own views reads the coefficient buffer in place; the
+    gradient must equal the concatenating path's when the loss also uses the
+    coefficients and a block is modified in place before the inverse."""
+    rs = np.random.RandomState(5)
+    x = gpu(rs.standard_normal((2, 3, N)))
+    tgt = gpu(rs.standard_normal((2, 3, N)))
+    grads = []
+    for copy in (False, True):
+        xg = x.clone().requires_grad_(True)
+        bl, sd = train.fwd(xg)
+        bl[1].mul_(0.5)                                   # in place on a view
+        if copy:                                          # separate tensors: the concatenating path
+            bl, sd = [c.clone() for c in bl], [c.clone() for c in sd]
+        y = train.bwd(bl, sd)
+        assert y.shape == x.shape
+        loss = ((y - tgt) ** 2).mean() + sum((c.abs() ** 2).mean() for c in bl[:3])
+        loss.backward()
+        grads.append(cnp(xg.grad))
+    assert snr_db(grads[1], grads[0]) >= 120
+
+
 # ---------------------------------------------------------- graph replay
 
 def test_graph_replay_rebuilds_poisoned_outputs(fused):
