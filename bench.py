@@ -320,7 +320,7 @@ def kernel_timings(f, B, reps):
     return out
 
 
-KERNEL_SYMBOL = {"packed_fft": ("k_col_fwd", "k_row_fwd"), "route_bands": ("k_route_bands<0>",),
+KERNEL_SYMBOL = {"packed_fft": ("k_col_fwd<false>", "k_row_fwd"), "route_bands": ("k_route_bands<0>",),
                  "scatter_bands": ("k_scatter_bands<0>",), "packed_ifft": ("k_col_inv", "k_row_inv")}
 
 
