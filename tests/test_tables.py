@@ -138,3 +138,24 @@ def test_scatter_slots_unique_and_fold_lists(factored_tables):
             for e in fold[w * T.FOLD_PER_WG:(w + 1) * T.FOLD_PER_WG]:
                 if e >= 0 and (e & 0xFFFF) != T.L:
                     assert T.inverse_column_wg(int(e) & 255) == w
+
+
+def test_trainable_base_detection_cpu():
+    """TrainableCQT.bwd reads the coefficient buffer in place only for fwd's
+    own consecutive group views; anything else takes the concatenating path."""
+    import torch
+    from flash_cqt.trainable import TrainableCQT
+    eng = TrainableCQT.__new__(TrainableCQT)           # host logic only, no GPU engine
+    eng.dev = torch.device("cpu")
+    eng.gspec = [(2, 4, 0), (3, 8, 8), (1, 16, 32)]
+    eng.ncoef = 48
+    B = 3
+    kc = torch.zeros(B, eng.ncoef, dtype=torch.complex64)
+    views = [kc.narrow(1, off, b * M).view(B, b, M) for b, M, off in eng.gspec]
+    assert eng._base_of(views, B) is kc
+    assert eng._base_of([v.clone() for v in views], B) is None           # copies
+    assert eng._base_of([views[1], views[0], views[2]], B) is None        # order
+    assert eng._base_of(views, B + 1) is None                             # batch
+    other = torch.zeros(B, eng.ncoef, dtype=torch.complex64)
+    mixed = [views[0], other.narrow(1, 8, 24).view(B, 3, 8), views[2]]
+    assert eng._base_of(mixed, B) is None                                 # two buffers
