@@ -74,6 +74,9 @@ class SlicedCQT:
             self.cqt = oct_
         self.tw = makewnd(sl_len, tr_area, device=device, dtype=dtype)
         self._roll = [m // 4 for m in self.size_per_oct]
+        # run the framing inside the HIP engine's kernels when it can (False:
+        # always frame on the host around self.cqt, as the reference does)
+        self.fused_framing = True
 
     # ------------------------------------------------------------ latency
 
@@ -132,8 +135,10 @@ class SlicedCQT:
     # ------------------------------------------- fused framing (HIP engine)
 
     def _fused(self, *tensors):
-        """The HIP engine when the framing can run inside it: engine is
-        TrainableCQT, inputs on its GPU, and no gradient is being recorded."""
+        """The HIP engine when the framing can run inside it: enabled, engine
+        is TrainableCQT, inputs on its GPU, and no gradient is being recorded."""
+        if not self.fused_framing:
+            return None
         f = getattr(self.cqt, "f", None)
         if type(self.cqt).__name__ != "TrainableCQT" or f is None:
             return None

@@ -381,11 +381,11 @@ def test_sliced_fused_ragged_lengths(length):
         bl, sd = s.fwd(x)
         y = s.bwd(bl, sd, length=length)
         yfull = s.bwd(bl, sd)
-        s._fused = lambda *a: None              # host framing around the same engine
+        s.fused_framing = False              # host framing around the same engine
         bl2, sd2 = s.fwd(x)
         y2 = s.bwd(bl2, sd2, length=length)
         yfull2 = s.bwd(bl2, sd2)
-        del s._fused
+        s.fused_framing = True
     S = s._num_slices(length)
     assert bl[0].shape[-1] == S * s.size_per_oct[0] and sd[0].shape[2] == S
     for a, b in zip(bl + sd, bl2 + sd2):
