@@ -260,3 +260,52 @@ class FusedOctCQT:
         """Complex per-group blocks [B, bins, M] built from the planes."""
         return [torch.complex(KR[:, off:off + b * M], KI[:, off:off + b * M]).view(-1, b, M)
                 for b, M, off in self.gspec]
+
+    # --------------------------------------- reference entry points kept
+
+    def persist_fwd(self, x):
+        """The reference's single-launch forward (fused.py:748-762). On MI355X
+        a cooperative launch alone costs more than this engine's three
+        forward kernels, so this runs fwd; same outputs (workspace views)."""
+        return self.fwd(x)
+
+    def persist_inv(self, KR, KI):
+        """The reference's single-launch inverse (fused.py:764-778); runs bwd."""
+        return self.bwd(KR, KI)
+
+    def bench_parts(self, x, reps=50):
+        """Median ms per engine part for input x [B, 65536], each part
+        graph-captured and replayed (diagnosis, as the reference's
+        bench_parts, fused.py:1082): the two forward FFT passes, the route
+        + band IDFT kernel, the band DFT + scatter kernel, the two inverse
+        FFT passes."""
+        self._check_x(x)
+        B = x.shape[0]
+        w = self._workspace(B)
+        self.bwd(*self.fwd(x))
+
+        def med(fn):
+            s = torch.cuda.Stream(self.dev)
+            s.wait_stream(torch.cuda.current_stream(self.dev))
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream(self.dev).wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn()
+            ts = []
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            for _ in range(reps):
+                a.record()
+                g.replay()
+                b.record()
+                b.synchronize()
+                ts.append(a.elapsed_time(b))
+            ts.sort()
+            return ts[len(ts) // 2]
+
+        return [("fwd packed fft", med(lambda: self.packed_fft(x, w["X"], w["W"]))),
+                ("fwd route + band idft", med(lambda: self.route_bands(w["X"], w["KR"], w["KI"], _native.PLANAR))),
+                ("inv band dft + scatter", med(lambda: self.scatter_bands(w["KR"], w["KI"], _native.PLANAR, w["F"]))),
+                ("inv packed ifft", med(lambda: self.packed_ifft(w["F"], w["XO"], w["W"])))]

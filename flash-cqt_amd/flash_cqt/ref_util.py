@@ -39,17 +39,18 @@ def window_ranges(lengths, centre_bins, total):
     return out, nn
 
 
-def painless_dual(windows, ranges, nn, block_lengths):
-    """Canonical dual windows of a painless frame, float32.
+def painless_dual(windows, ranges, nn, block_lengths, dtype=np.float32):
+    """Canonical dual windows of a painless frame (diagonal in `dtype`,
+    float32 as the reference bank uses).
 
     The frame operator is diagonal: d[k] = sum_i M_i |g_i(k)|^2 over the
     windows covering bin k (g in natural order), and the dual of window i is
     g_i / d over its own support, back in fft order (ref_util.py:46-55).
     Returns (duals, diagonal).
     """
-    d = np.zeros(nn, dtype=np.float32)
+    d = np.zeros(nn, dtype=dtype)
     for g, m, rng in zip(windows, block_lengths, ranges):
-        d[rng] = d[rng] + np.square(np.fft.fftshift(g)) * np.float32(m)
+        d[rng] = d[rng] + np.square(np.fft.fftshift(g)) * dtype(m)
     duals = [g / np.fft.ifftshift(d[rng]) for g, rng in zip(windows, ranges)]
     return duals, d
 
@@ -59,3 +60,26 @@ def hannwin(l, device="cpu"):
     """Reference-compatible alias: float64 torch Hann window (ref_util.py:19)."""
     import torch
     return torch.as_tensor(hann_fft_order(l), device=torch.device(device))
+
+
+def calcwinrange(g, rfbas, Ls, device="cpu"):
+    """Reference-compatible: (index ranges as int64 tensors, nn) of windows g
+    centred at the bins rfbas (ref_util.py:28-43); window_ranges does the work."""
+    import torch
+    ranges, nn = window_ranges([len(gi) for gi in g], np.asarray(rfbas), Ls)
+    return [torch.as_tensor(r, device=torch.device(device)) for r in ranges], nn
+
+
+def nsdual(g, wins, nn, M=None, dtype=None, device="cpu"):
+    """Reference-compatible: dual windows (torch tensors) of windows g over
+    ranges wins with block lengths M (ref_util.py:46-55); the frame diagonal
+    accumulates in `dtype` (float32 by default, as the reference's)."""
+    import torch
+    if M is None:
+        raise ValueError("nsdual needs the block lengths M")
+    dt = {torch.float64: np.float64, torch.float32: np.float32, None: np.float32}[dtype]
+    gn = [gi.detach().cpu().numpy() if torch.is_tensor(gi) else np.asarray(gi) for gi in g]
+    wn = [w.detach().cpu().numpy() if torch.is_tensor(w) else np.asarray(w) for w in wins]
+    mn = [int(m) for m in (M.tolist() if torch.is_tensor(M) else M)]
+    duals, _ = painless_dual(gn, wn, int(nn), mn, dtype=dt)
+    return [torch.as_tensor(d, device=torch.device(device)) for d in duals]

@@ -415,6 +415,21 @@ def test_sliced_config5_round_trip():
     assert db >= 125
 
 
+def test_reference_entry_points(fused):
+    """persist_fwd / persist_inv give fwd / bwd's results; bench_parts names
+    and times the four engine parts."""
+    x, _ = inputs()
+    xg = gpu(x)
+    KR, KI = fused.fwd(xg)
+    k = torch.complex(KR, KI).clone()
+    y = fused.bwd(KR, KI).clone()
+    PR, PI = fused.persist_fwd(xg)
+    assert torch.equal(torch.complex(PR, PI), k)
+    assert torch.equal(fused.persist_inv(PR, PI), y)
+    parts = fused.bench_parts(xg, reps=5)
+    assert [p[0] for p in parts][1] == "fwd route + band idft" and all(p[1] > 0 for p in parts)
+
+
 # ------------------------------------------------------------- errors
 
 def test_bad_inputs_rejected(fused):

@@ -7,6 +7,7 @@ factored tables, replayed through the kernels' exact schedule
 both adjoints (the analogue of the reference's CPU table gates,
 bench/radix_gpu.py:51-120 and bench/autograd_check.py)."""
 import numpy as np
+import pytest
 import torch
 
 import kernel_sim as ks
@@ -159,3 +160,21 @@ def test_trainable_base_detection_cpu():
     other = torch.zeros(B, eng.ncoef, dtype=torch.complex64)
     mixed = [views[0], other.narrow(1, 8, 24).view(B, 3, 8), views[2]]
     assert eng._base_of(mixed, B) is None                                 # two buffers
+
+
+def test_reference_named_window_helpers_cpu():
+    """flash_cqt.ref_util.calcwinrange / nsdual (the reference's names and
+    signatures, torch in and out) equal the pinned oracle's on the bank."""
+    import torch
+    from oracle import cqt_oracle as co
+    from flash_cqt import ref_util as R
+    b = co.FlexOctBank([3, 4, 2], [8, 16, 32], fs=44100, audio_len=65536)
+    g = [torch.as_tensor(gi) for gi in b.g]
+    wins, nn = R.calcwinrange(g, b.rfbas, 65536)
+    assert nn == b.nn and all(np.array_equal(w.numpy(), ow) for w, ow in zip(wins, b.wins))
+    gd = R.nsdual(g, wins, nn, torch.as_tensor(b.M))
+    assert all(np.array_equal(d.numpy().view(np.uint32) if d.dtype == torch.float32 else d.numpy(),
+                              od.view(np.uint32) if od.dtype == np.float32 else od)
+               for d, od in zip(gd, b.gd))
+    with pytest.raises(ValueError):
+        R.nsdual(g, wins, nn)
