@@ -68,6 +68,9 @@ class FusedOctCQT:
             tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(),
             ntasks=int(tb["tasks"].shape[0]), ncoef=int(self.ncoef))
         self._tp = {k: v.data_ptr() for k, v in tb.items()}
+        # the reference exposes its band-engine tables as .radix (fused.py:430);
+        # here the same name holds this engine's tables (formats in tables.py)
+        self.radix = self.tables
         self._ws = {}
         self._wp = {}
 
