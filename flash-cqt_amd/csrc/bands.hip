@@ -50,12 +50,15 @@ constexpr int kBandLds = cmax(cmax(cmax(band_lds(32), band_lds(64)), cmax(band_l
 // slice s at ((sig bins_g + i) S + s) M, and in octave groups (roll flag)
 // output m of the band transform sits at (m + M/4) mod M in even slices and
 // (m - M/4) mod M in odd slices (the SlicedCQT quarter roll; side groups are
-// [nsig][S][1][M] blocks, unrolled).
+// [nsig][S][1][M] blocks, unrolled). Parity is that of the slice's index in
+// its signal, first + s, where first is the index of the call's first slice
+// (0 for a whole signal; the slice count so far when streaming).
 constexpr int kSliced = 2;
 
 struct SliceMap {
     const int4* __restrict__ groups;   // per task {off_g, bins_g, roll, 0}
-    int S;                             // slices per signal
+    int S;                             // slices per signal in this call
+    int first;                         // index in the signal of the call's slice 0
 };
 
 template <int M, int LAYOUT>
@@ -68,7 +71,7 @@ __device__ __forceinline__ void unit_coef(const int4 task, const int task_id, co
         const int s = b - sig * sm.S;
         const int i = (task.y - g.x) / M + u;
         base = (long)batch * g.x + ((long)(sig * g.y + i) * sm.S + s) * M;
-        shift = g.z ? ((s & 1) ? M - M / 4 : M / 4) : 0;
+        shift = g.z ? (((sm.first + s) & 1) ? M - M / 4 : M / 4) : 0;
     } else {
         base = (long)b * ncoef + task.y + u * M;
         shift = 0;
@@ -278,10 +281,10 @@ extern "C" int fcqt_route_bands(const fcqt_tables* tab, const int32_t* route, co
     const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
     if (layout == FCQT_PLANAR)
         hipLaunchKernelGGL(k_route_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, xx, coef_re,
-                           coef_im, rr, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
+                           coef_im, rr, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1, 0}, ws);
     else
         hipLaunchKernelGGL(k_route_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream, xx,
-                           coef_re, coef_re, rr, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
+                           coef_re, coef_re, rr, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1, 0}, ws);
     return launch_status();
 }
 
@@ -297,17 +300,18 @@ extern "C" int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat, c
     const auto* ws = reinterpret_cast<const float2*>(tab->tw_stage);
     if (layout == FCQT_PLANAR)
         hipLaunchKernelGGL(k_scatter_bands<FCQT_PLANAR>, grid, dim3(kBandThreads), 0, stream, coef_re,
-                           coef_im, f, ss, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
+                           coef_im, f, ss, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1, 0}, ws);
     else
         hipLaunchKernelGGL(k_scatter_bands<FCQT_INTERLEAVED>, grid, dim3(kBandThreads), 0, stream,
-                           coef_re, coef_re, f, ss, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1}, ws);
+                           coef_re, coef_re, f, ss, tt, (int)batch, (long)tab->ncoef, SliceMap{nullptr, 1, 0}, ws);
     return launch_status();
 }
 
 extern "C" int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
                                        const float* xs, float* coef, int64_t nsig, int64_t nslices,
-                                       hipStream_t stream) {
+                                       int64_t first, hipStream_t stream) {
     if (nsig < 1 || nslices < 1 || nsig > kMaxBatch || nslices > kMaxBatch) return FCQT_EARG;
+    if (first < 0 || first > kMaxBatch) return FCQT_EARG;
     const int64_t batch = nsig * nslices;
     if (int e = check_band_args(tab, route, coef, coef, FCQT_INTERLEAVED, batch)) return e;
     if (!xs || !groups) return FCQT_EARG;
@@ -316,15 +320,16 @@ extern "C" int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* ro
     hipLaunchKernelGGL(k_route_bands<kSliced>, grid, dim3(kBandThreads), 0, stream,
                        reinterpret_cast<const float2*>(xs), coef, coef, reinterpret_cast<const int2*>(route),
                        reinterpret_cast<const int4*>(tab->tasks), (int)batch, (long)tab->ncoef,
-                       SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices},
+                       SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices, (int)first},
                        reinterpret_cast<const float2*>(tab->tw_stage));
     return launch_status();
 }
 
 extern "C" int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
                                          const float* coef, float* f, int64_t nsig, int64_t nslices,
-                                         hipStream_t stream) {
+                                         int64_t first, hipStream_t stream) {
     if (nsig < 1 || nslices < 1 || nsig > kMaxBatch || nslices > kMaxBatch) return FCQT_EARG;
+    if (first < 0 || first > kMaxBatch) return FCQT_EARG;
     const int64_t batch = nsig * nslices;
     if (int e = check_band_args(tab, scat, coef, coef, FCQT_INTERLEAVED, batch)) return e;
     if (!f || !groups) return FCQT_EARG;
@@ -332,7 +337,7 @@ extern "C" int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* 
     const dim3 grid((unsigned)(tab->ntasks * batch));
     hipLaunchKernelGGL(k_scatter_bands<kSliced>, grid, dim3(kBandThreads), 0, stream, coef, coef, f,
                        reinterpret_cast<const int2*>(scat), reinterpret_cast<const int4*>(tab->tasks),
-                       (int)batch, (long)tab->ncoef, SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices},
+                       (int)batch, (long)tab->ncoef, SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices, (int)first},
                        reinterpret_cast<const float2*>(tab->tw_stage));
     return launch_status();
 }

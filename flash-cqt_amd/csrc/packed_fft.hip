@@ -48,16 +48,21 @@ __device__ __forceinline__ float2 dense_bin(const float2* __restrict__ fb, int i
 }
 
 // SlicedCQT framing read by the sliced column pass: batch row sig * S + s is
-// slice s of signal sig, sample j = x[sig][2H (s - 1) + jj] win[jj] with
-// jj = (j + H) mod N in even slices and (j - H) mod N in odd slices
-// (H = N/4; samples outside the signal are zero). This is the zero padding,
-// 50%-overlap unfold, Tukey window and quarter roll of the reference
-// SlicedCQT._slice in one read.
+// slice g = first + s of signal sig, sample j = x[2H (g - 1) + jj] win[jj]
+// with jj = (j + H) mod N in even slices g and (j - H) mod N in odd ones
+// (H = N/4; samples outside the signal are zero). The call holds the signal
+// from sample `origin` on: x[i] = sig[sig][i - origin] for
+// 0 <= i - origin < len (a whole signal: first = origin = 0; one streamed
+// slice g from a buffer holding exactly its N samples: first = g,
+// origin = 2H (g - 1)). This is the zero padding, 50%-overlap unfold, Tukey
+// window and quarter roll of the reference SlicedCQT._slice in one read.
 struct SliceSrc {
     const float* sig;   // [nsig][len]
     const float* win;   // [N]
     long len;
     int S;
+    long first;         // index in the signal of the call's slice 0
+    long origin;        // signal sample index of sig[.][0]
 };
 
 constexpr int kQuarter = kN / 4;
@@ -93,8 +98,9 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
         const int sig = b / src.S;
         const int sl = b - sig * src.S;
         const float* xrow = src.sig + (long)sig * src.len;
-        const long s0 = 2l * kQuarter * (sl - 1);
-        const int sh = (sl & 1) ? kN - kQuarter : kQuarter;
+        const long g = src.first + sl;
+        const long s0 = 2l * kQuarter * (g - 1) - src.origin;
+        const int sh = (g & 1) ? kN - kQuarter : kQuarter;
 #pragma unroll
         for (int r = 0; r < 16; ++r) v[r] = sliced_pair(src, xrow, s0, sh, 256 * (t + 8 * r) + n2);
     } else {
@@ -342,7 +348,7 @@ extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
     hipLaunchKernelGGL(k_col_fwd<false>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
                        reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
-                       reinterpret_cast<const float2*>(tab->tw_pass), tws, SliceSrc{nullptr, nullptr, 1, 1});
+                       reinterpret_cast<const float2*>(tab->tw_pass), tws, SliceSrc{nullptr, nullptr, 1, 1, 0, 0});
     if (int e = launch_status()) return e;
     hipLaunchKernelGGL(k_row_fwd, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
                        reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(xs),
@@ -369,8 +375,11 @@ extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, c
 }
 
 extern "C" int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int64_t sig_len, const float* window,
-                                  int64_t nsig, int64_t nslices, float* xs, float* work, hipStream_t stream) {
+                                  int64_t nsig, int64_t nslices, int64_t first, int64_t origin, float* xs,
+                                  float* work, hipStream_t stream) {
     if (!tab || !sig || !window || !xs || !work || sig_len < 1 || nsig < 1 || nslices < 1) return FCQT_EARG;
+    if (first < 0 || first > kMaxBatch || origin < -(int64_t)kN || origin > (int64_t)kN * kMaxBatch)
+        return FCQT_EARG;
     if (nsig > kMaxBatch || nslices > kMaxBatch || nsig * nslices > kMaxBatch) return FCQT_EARG;
     if (!tab->tw_pass || !tab->tw_half || !tab->tw_stage) return FCQT_EARG;
     if (!aligned(sig, 4) || !aligned(window, 4) || !aligned(xs, 8) || !aligned(work, 8) ||
@@ -380,7 +389,7 @@ extern "C" int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int6
     const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
     hipLaunchKernelGGL(k_col_fwd<true>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
                        nullptr, reinterpret_cast<float2*>(work), reinterpret_cast<const float2*>(tab->tw_pass), tws,
-                       SliceSrc{sig, window, (long)sig_len, (int)nslices});
+                       SliceSrc{sig, window, (long)sig_len, (int)nslices, (long)first, (long)origin});
     if (int e = launch_status()) return e;
     hipLaunchKernelGGL(k_row_fwd, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
                        reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(xs),
@@ -413,6 +422,36 @@ __global__ __launch_bounds__(256) void k_overlap_add(const float* __restrict__ y
     out[(long)sig * length + p] = acc;
 }
 }  // namespace fcqt
+
+namespace fcqt {
+// Streamed overlap-add of one inverse slice g per signal (SlicedCQT.stream_bwd):
+// with y_r the slice rolled back (y_r[j] = y[(j - H) mod N] for even g,
+// y[(j + H) mod N] for odd g), out[p] = tail[p] + y_r[p] and
+// tail[p] = y_r[2H + p] for p < 2H; emit = 0 (the first slice) only fills tail.
+__global__ __launch_bounds__(256) void k_stream_overlap(const float* __restrict__ y, float* __restrict__ tail,
+                                                        float* __restrict__ out, int odd, int emit) {
+    const int p = (int)blockIdx.x * 256 + (int)threadIdx.x;   // < 2H: the grid is exact
+    const long sig = blockIdx.y;
+    const int sh = odd ? kQuarter : kN - kQuarter;
+    const float* yr = y + sig * kN;
+    float* tr = tail + sig * 2 * kQuarter;
+    const float a = yr[(p + sh) & (kN - 1)];
+    const float b = yr[(p + 2 * kQuarter + sh) & (kN - 1)];
+    if (emit) out[sig * 2 * kQuarter + p] = tr[p] + a;
+    tr[p] = b;
+}
+}  // namespace fcqt
+
+extern "C" int fcqt_stream_overlap(const float* y, float* tail, float* out, int64_t nsig, int64_t slice,
+                                   hipStream_t stream) {
+    if (!y || !tail || nsig < 1 || nsig > 65535 || slice < 0) return FCQT_EARG;
+    if (slice > 0 && !out) return FCQT_EARG;
+    if (!aligned(y, 4) || !aligned(tail, 4) || (out && !aligned(out, 4))) return FCQT_EALIGN;
+    static_assert((2 * kQuarter) % 256 == 0, "exact grid");
+    hipLaunchKernelGGL(k_stream_overlap, dim3((unsigned)(2 * kQuarter / 256), (unsigned)nsig), dim3(256), 0, stream,
+                       y, tail, out, (int)(slice & 1), slice > 0 ? 1 : 0);
+    return launch_status();
+}
 
 extern "C" int fcqt_overlap_add(const float* y, float* out, int64_t nsig, int64_t nslices, int64_t length,
                                 hipStream_t stream) {

@@ -12,7 +12,7 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 PLANAR = 0
 INTERLEAVED = 1
 
@@ -21,7 +21,7 @@ EXPORTS = ("fcqt_abi_version", "fcqt_status_string", "fcqt_last_hip_error",
            "fcqt_packed_fft_fwd", "fcqt_route_bands", "fcqt_scatter_bands",
            "fcqt_packed_fft_inv", "fcqt_analysis", "fcqt_synthesis", "fcqt_fill_zero",
            "fcqt_slice_fft_fwd", "fcqt_route_bands_sliced", "fcqt_scatter_bands_sliced",
-           "fcqt_overlap_add")
+           "fcqt_overlap_add", "fcqt_stream_overlap")
 
 
 class Tables(ctypes.Structure):
@@ -63,10 +63,11 @@ def load():
         "fcqt_analysis": ([T, P, P, P, P, ctypes.c_int, P, P, I64, S], ctypes.c_int),
         "fcqt_synthesis": ([T, P, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
         "fcqt_fill_zero": ([P, I64, S], ctypes.c_int),
-        "fcqt_slice_fft_fwd": ([T, P, I64, P, I64, I64, P, P, S], ctypes.c_int),
-        "fcqt_route_bands_sliced": ([T, P, P, P, P, I64, I64, S], ctypes.c_int),
-        "fcqt_scatter_bands_sliced": ([T, P, P, P, P, I64, I64, S], ctypes.c_int),
+        "fcqt_slice_fft_fwd": ([T, P, I64, P, I64, I64, I64, I64, P, P, S], ctypes.c_int),
+        "fcqt_route_bands_sliced": ([T, P, P, P, P, I64, I64, I64, S], ctypes.c_int),
+        "fcqt_scatter_bands_sliced": ([T, P, P, P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_overlap_add": ([P, P, I64, I64, I64, S], ctypes.c_int),
+        "fcqt_stream_overlap": ([P, P, P, I64, I64, S], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

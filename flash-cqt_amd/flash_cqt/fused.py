@@ -184,9 +184,10 @@ class FusedOctCQT:
 
     # ------------------------------------------- SlicedCQT framing
 
-    def slice_fft(self, sig, window, nslices, xs, work):
-        """X of every 65536-sample slice of the signals sig [nsig, len]
-        (SlicedCQT framing: zero pad, 50% overlap, window, quarter roll)."""
+    def slice_fft(self, sig, window, nslices, xs, work, first=0, origin=0):
+        """X of slices first .. first + nslices - 1 of the signals sig [nsig, len]
+        (SlicedCQT framing: zero pad, 50% overlap, window, quarter roll);
+        sig[:, 0] is signal sample `origin` (0 for a whole signal)."""
         if sig.dim() != 2 or sig.shape[1] < 1:
             raise ValueError("sig must be [nsig, len]")
         nsig, length = sig.shape
@@ -196,28 +197,40 @@ class FusedOctCQT:
         self._need(xs, B * T.XSTRIDE * 8, "xs")
         self._need(work, B * L * 8, "work")
         _native.check(self.lib.fcqt_slice_fft_fwd(self._ct, _native.ptr(sig), length, _native.ptr(window), nsig,
-                                                  nslices, _native.ptr(xs), _native.ptr(work),
+                                                  nslices, first, origin, _native.ptr(xs), _native.ptr(work),
                                                   _native.stream_handle(self.dev.index)), "slice_fft_fwd")
 
-    def route_bands_sliced(self, xs, coef, nsig, nslices, table="route"):
+    def route_bands_sliced(self, xs, coef, nsig, nslices, table="route", first=0):
         """Coefficients of every slice into the SlicedCQT block layout
-        (complex64, nsig * nslices * ncoef values)."""
+        (complex64, nsig * nslices * ncoef values); `first` is the signal
+        index of the call's first slice (its parity sets the quarter roll)."""
         B = nsig * nslices
         self._need(xs, B * T.XSTRIDE * 8, "xs")
         self._need(coef, B * self.ncoef * 8, "coef")
         _native.check(self.lib.fcqt_route_bands_sliced(self._ct, _native.ptr(self.tables[table]),
                                                        _native.ptr(self.tables["slice_groups"]), _native.ptr(xs),
-                                                       _native.ptr(coef), nsig, nslices,
+                                                       _native.ptr(coef), nsig, nslices, first,
                                                        _native.stream_handle(self.dev.index)), "route_bands_sliced")
 
-    def scatter_bands_sliced(self, coef, f, nsig, nslices, table="scat"):
+    def scatter_bands_sliced(self, coef, f, nsig, nslices, table="scat", first=0):
         B = nsig * nslices
         self._need(coef, B * self.ncoef * 8, "coef")
         self._need(f, B * T.FROW * 8, "f")
         _native.check(self.lib.fcqt_scatter_bands_sliced(self._ct, _native.ptr(self.tables[table]),
                                                          _native.ptr(self.tables["slice_groups"]),
-                                                         _native.ptr(coef), _native.ptr(f), nsig, nslices,
+                                                         _native.ptr(coef), _native.ptr(f), nsig, nslices, first,
                                                          _native.stream_handle(self.dev.index)), "scatter_bands_sliced")
+
+    def stream_overlap(self, y, tail, out, nsig, slice_index):
+        """One streamed slice's half-slice overlap-add: out = tail + y rolled
+        back (first half), tail = its second half; out unused for slice 0."""
+        self._need(y, nsig * N * 4, "y")
+        self._need(tail, nsig * HALF * 4, "tail")
+        if slice_index > 0:
+            self._need(out, nsig * HALF * 4, "out")
+        _native.check(self.lib.fcqt_stream_overlap(_native.ptr(y), _native.ptr(tail),
+                                                   _native.ptr(out if slice_index > 0 else None), nsig, slice_index,
+                                                   _native.stream_handle(self.dev.index)), "stream_overlap")
 
     def overlap_add(self, y, out, nsig, nslices, length):
         self._need(y, nsig * nslices * N * 4, "y")

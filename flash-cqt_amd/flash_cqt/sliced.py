@@ -150,16 +150,22 @@ class SlicedCQT:
         return f
 
     def _ws(self, f, nsig, S):
+        """Engine buffers per (signals, slices per call); F is zeroed once."""
+        cache = self.__dict__.setdefault("_fused_ws", {})
         key = (nsig, S)
-        ws = getattr(self, "_fused_ws", None)
-        if ws is None or ws[0] != key:
+        if key not in cache:
             from . import tables as T
             B = nsig * S
             dev = f.dev
-            ws = (key, dict(X=torch.empty(B, T.XSTRIDE, 2, device=dev), W=torch.empty(B, T.L, 2, device=dev),
-                            F=torch.zeros(B, T.FROW, 2, device=dev), Y=torch.empty(B, self.sl_len, device=dev)))
-            self._fused_ws = ws
-        return ws[1]
+            cache[key] = dict(X=torch.empty(B, T.XSTRIDE, 2, device=dev), W=torch.empty(B, T.L, 2, device=dev),
+                              F=torch.zeros(B, T.FROW, 2, device=dev), Y=torch.empty(B, self.sl_len, device=dev))
+        return cache[key]
+
+    def _tw32(self):
+        tw = self.__dict__.get("_tw32_cache")
+        if tw is None:
+            tw = self.__dict__["_tw32_cache"] = self.tw.to(torch.float32).contiguous()
+        return tw
 
     def _fwd_fused(self, f, x):
         B, C, L = x.shape
@@ -167,7 +173,7 @@ class SlicedCQT:
         nsig = B * C
         sig = x.reshape(nsig, L).to(torch.float32).contiguous()
         ws = self._ws(f, nsig, S)
-        f.slice_fft(sig, self.tw.to(torch.float32).contiguous(), S, ws["X"], ws["W"])
+        f.slice_fft(sig, self._tw32(), S, ws["X"], ws["W"])
         coef = torch.empty(nsig * S * f.ncoef, dtype=torch.complex64, device=f.dev)
         f.route_bands_sliced(ws["X"], coef, nsig, S)
         ng = len(self.oct_bins)
@@ -182,12 +188,16 @@ class SlicedCQT:
 
     def _block_buffer(self, f, blocks, side, nsig, S):
         """One complex64 buffer in the fused block layout: the blocks' own
-        storage when they are the views _fwd_fused returned, else a copy."""
+        storage when they are the views the fused forward returned (views of
+        one buffer at the group offsets), else a copy."""
         parts = list(blocks) + (list(side) if side is not None else [])
-        if side is not None and all(p.dtype == torch.complex64 and p.is_contiguous() for p in parts):
-            base = parts[0].data_ptr()
-            if all(p.data_ptr() == base + 8 * nsig * S * off for p, (_, _, off) in zip(parts, f.gspec)):
-                return torch.as_strided(parts[0], (nsig * S * f.ncoef,), (1,))
+        base = parts[0]._base
+        if side is not None and base is not None and base.dim() == 1 and base.dtype == torch.complex64 \
+                and base.numel() == nsig * S * f.ncoef and base.device == f.dev and base.is_contiguous():
+            ptr = base.data_ptr()
+            if all(p._base is base and p.is_contiguous() and p.data_ptr() == ptr + 8 * nsig * S * off
+                   for p, (_, _, off) in zip(parts, f.gspec)):
+                return base
         coef = torch.zeros(nsig * S * f.ncoef, dtype=torch.complex64, device=f.dev)
         for p, (b, M, off) in zip(parts, f.gspec):
             coef[nsig * S * off:nsig * S * (off + b * M)] = p.reshape(-1).to(torch.complex64)
@@ -244,6 +254,32 @@ class SlicedCQT:
         return out[..., :length] if length is not None else out
 
     # --------------------------------------------- streaming, bounded state
+    # With the HIP engine each streamed slice k is one fused call: the slice
+    # is framed from [previous chunk, chunk] by the column pass (first = k,
+    # origin = hop (k - 1)), its coefficients are stored straight into the
+    # per-slice block layout, and the inverse rolls and overlap-adds in one
+    # kernel that carries the half-slice tail. Same values as the host
+    # framing below, which runs when the engine cannot (autograd, torch engine).
+
+    def _stream_slice_fused(self, f, prev, chunk, k):
+        B, C, hop = chunk.shape
+        nsig = B * C
+        buf = torch.cat([prev, chunk], dim=-1).reshape(nsig, 2 * hop).to(torch.float32).contiguous()
+        ws = self._ws(f, nsig, 1)
+        f.slice_fft(buf, self._tw32(), 1, ws["X"], ws["W"], first=k, origin=hop * (k - 1))
+        coef = torch.empty(nsig * f.ncoef, dtype=torch.complex64, device=f.dev)
+        f.route_bands_sliced(ws["X"], coef, nsig, 1, first=k)
+        ng = len(self.oct_bins)
+        views = [coef[nsig * off:nsig * (off + b * M)].view(B, C, b, M) for b, M, off in f.gspec]
+        return views[:ng], views[ng:]
+
+    def _stream_slice_host(self, prev, chunk, k):
+        sl = torch.cat([prev, chunk], dim=-1) * self.tw
+        sl = torch.roll(sl, -self.H if k % 2 == 0 else self.H, -1)
+        blocks, side = self.cqt.fwd(sl.unsqueeze(2))
+        # a single slice is "even" for _arrange; odd slices roll the other way
+        blocks = self._arrange(blocks, 1, fwd=(k % 2 == 0))
+        return [c[:, :, 0] for c in blocks], [c[:, :, 0] for c in side]
 
     def stream_fwd(self, chunks):
         """chunks yields [B, C, hop] pieces (pad the last one); yields one
@@ -253,12 +289,10 @@ class SlicedCQT:
         k = 0
 
         def one(prev, chunk, k):
-            sl = torch.cat([prev, chunk], dim=-1) * self.tw
-            sl = torch.roll(sl, -self.H if k % 2 == 0 else self.H, -1)
-            blocks, side = self.cqt.fwd(sl.unsqueeze(2))
-            # a single slice is "even" for _arrange; odd slices roll the other way
-            blocks = self._arrange(blocks, 1, fwd=(k % 2 == 0))
-            return [c[:, :, 0] for c in blocks], [c[:, :, 0] for c in side]
+            f = self._fused(prev, chunk)
+            if f is not None and chunk.shape[-1] == self.hop:
+                return self._stream_slice_fused(f, prev, chunk, k)
+            return self._stream_slice_host(prev, chunk, k)
 
         for chunk in chunks:
             if prev is None:
@@ -270,16 +304,35 @@ class SlicedCQT:
 
     def stream_bwd(self, slice_coeffs):
         """slice_coeffs yields (blocks, side) as stream_fwd emits; yields
-        [B, C, hop] output pieces one slice behind. State: one half slice."""
+        [B, C, hop] output pieces one slice behind. State: one half slice
+        (the rolled second half of the last inverse slice)."""
         tail = None
         k = 0
         for blocks, side in slice_coeffs:
+            f = self._fused(*blocks, *(side if side is not None else []))
+            B, C = blocks[0].shape[:2]
+            if f is not None:
+                nsig = B * C
+                if tail is None:
+                    tail = torch.zeros(B, C, self.hop, dtype=torch.float32, device=f.dev)
+                elif not (tail.is_contiguous() and tail.dtype == torch.float32 and tail.device == f.dev):
+                    tail = tail.to(device=f.dev, dtype=torch.float32).contiguous()
+                coef = self._block_buffer(f, blocks, side, nsig, 1)
+                ws = self._ws(f, nsig, 1)
+                f.scatter_bands_sliced(coef, ws["F"], nsig, 1, first=k)
+                f.packed_ifft(ws["F"], ws["Y"], ws["W"])
+                out = torch.empty(B, C, self.hop, dtype=torch.float32, device=f.dev) if k > 0 else None
+                f.stream_overlap(ws["Y"], tail, out, nsig, k)
+                if out is not None:
+                    yield out
+                k += 1
+                continue
             blocks = [c.unsqueeze(2) for c in blocks]
             side = [c.unsqueeze(2) for c in side] if side is not None else None
             blocks = self._arrange(blocks, 1, fwd=(k % 2 != 0))
             y = self.cqt.bwd(blocks, side)[:, :, 0]
             y = torch.roll(y, self.H if k % 2 == 0 else -self.H, -1)
-            if tail is not None:
+            if k > 0:
                 yield tail + y[..., :self.hop]
             tail = y[..., self.hop:]
             k += 1

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 5
+#define FCQT_ABI_VERSION 6
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -157,30 +157,38 @@ int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* o
                    float* f, float* work, float* y, int64_t batch, hipStream_t stream);
 
 /* ---- SlicedCQT framing fused into the engine (same kernels, other I/O) ----
- * nsig signals of sig_len samples, each cut into nslices 65536-sample slices
- * at hop N/2 (batch row sig * nslices + s); H = N/4.
+ * nsig signals, each cut into 65536-sample slices at hop N/2; one call
+ * handles nslices consecutive slices g = first + s, s < nslices, of every
+ * signal (batch row sig * nslices + s); H = N/4. A whole signal is one call
+ * with first = 0; streaming (SlicedCQT.stream_fwd/stream_bwd) makes one call
+ * per slice with first = the slice's index.
  *
- * Sliced real FFT: slice s of signal sig is x[sig][2H (s - 1) + jj] * window[jj]
- * with jj = (j + H) mod N for even s and (j - H) mod N for odd s (zero
- * outside the signal): the zero padding, 50%-overlap unfold, Tukey window
- * and quarter roll, read straight from the signal by the column pass.
+ * Sliced real FFT: slice g of signal sig is x[2H (g - 1) + jj] * window[jj]
+ * with jj = (j + H) mod N for even g and (j - H) mod N for odd g, where the
+ * call holds the signal from sample `origin` on (x[i] = sig[sig][i - origin]
+ * for 0 <= i - origin < sig_len, zero elsewhere): the zero padding,
+ * 50%-overlap unfold, Tukey window and quarter roll, read straight from the
+ * signal by the column pass. Whole signal: origin = 0; one streamed slice g
+ * from a buffer holding its N samples: origin = 2H (g - 1).
  *   sig    [nsig][sig_len] fp32,  window [65536] fp32
  *   xs, work as for fcqt_packed_fft_fwd with batch nsig * nslices
- * Replaces SlicedCQT._slice (sliced.py:106-117) + the pack copy and fft3. */
+ * Replaces SlicedCQT._slice (sliced.py:106-117) and the per-slice framing of
+ * stream_fwd (sliced.py:178-184) + the pack copy and fft3. */
 int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int64_t sig_len, const float* window,
-                       int64_t nsig, int64_t nslices, float* xs, float* work, hipStream_t stream);
+                       int64_t nsig, int64_t nslices, int64_t first, int64_t origin, float* xs,
+                       float* work, hipStream_t stream);
 
 /* Route + band IDFTs storing straight into the SlicedCQT block layout
  * (interleaved complex, nsig * nslices * ncoef values): group g (first
  * coefficient off_g, bins_g bands of length M, per-task table `groups`
  * [ntasks][4] = {off_g, bins_g, roll, 0}) is the block [nsig][bins_g][nslices * M]
  * at nsig * nslices * off_g; in octave groups (roll = 1) band output m of an
- * even slice goes to (m + M/4) mod M, of an odd slice to (m - M/4) mod M;
+ * even slice g goes to (m + M/4) mod M, of an odd slice to (m - M/4) mod M;
  * side groups are [nsig][nslices][1][M] blocks.
  * Replaces fwd_bands + SlicedCQT._arrange(fwd) and the block permute of
  * SlicedCQT.fwd (sliced.py:119-131, 134-146). */
 int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
-                            const float* xs, float* coef, int64_t nsig, int64_t nslices,
+                            const float* xs, float* coef, int64_t nsig, int64_t nslices, int64_t first,
                             hipStream_t stream);
 
 /* Band DFTs + slot scatter reading the same block layout (the inverse
@@ -188,7 +196,7 @@ int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* route, const 
  * Replaces the block permute + SlicedCQT._arrange(bwd) of SlicedCQT.bwd and
  * inv_bands (sliced.py:148-157). */
 int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
-                              const float* coef, float* f, int64_t nsig, int64_t nslices,
+                              const float* coef, float* f, int64_t nsig, int64_t nslices, int64_t first,
                               hipStream_t stream);
 
 /* Overlap-add of the inverse slices (y [nsig * nslices][65536], the output of
@@ -197,6 +205,17 @@ int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* scat, const
  * Replaces the roll, overlap-add and trim of SlicedCQT.bwd (sliced.py:158-166). */
 int fcqt_overlap_add(const float* y, float* out, int64_t nsig, int64_t nslices, int64_t length,
                      hipStream_t stream);
+
+/* Streamed overlap-add of one inverse slice g per signal (y [nsig][65536],
+ * the output of fcqt_packed_fft_inv for that slice): with the slice rolled
+ * back (+H for even g, -H for odd g) into y_r, out[sig][p] = tail[sig][p] +
+ * y_r[p] and then tail[sig][p] = y_r[2H + p], p < 2H. For g = 0 only tail is
+ * written (out may be NULL). tail [nsig][2H] starts at zero and carries the
+ * stream's state between calls.
+ * Replaces the roll and half-slice overlap-add of SlicedCQT.stream_bwd
+ * (sliced.py:194-209). */
+int fcqt_stream_overlap(const float* y, float* tail, float* out, int64_t nsig, int64_t slice,
+                        hipStream_t stream);
 
 /* Zero n floats with a fill kernel (graph-capture safe, no hipMemsetAsync). */
 int fcqt_fill_zero(float* buf, int64_t n, hipStream_t stream);

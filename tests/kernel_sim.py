@@ -376,3 +376,40 @@ def scatter_bands(C, scat, tasks, ncoef):
     tl = target[gr != 0]
     assert np.unique(tl).size == tl.size, "two taps share a slot"
     return F
+
+
+# ---------------------------------------------------------------- sliced framing
+
+def sliced_frames(sig, win, S, first=0, origin=0):
+    """The sliced column pass's read, index for index (sliced_pair in
+    packed_fft.hip): slice g = first + s of each signal row, sample j =
+    x[2H (g - 1) + jj] win[jj], jj = (j + H) mod N for even g and (j - H)
+    mod N for odd g, x[i] = sig[i - origin] inside the row and 0 outside.
+    Returns [nsig * S, N] float32 and asserts every clamped read in range."""
+    H = N // 4
+    nsig, length = sig.shape
+    out = np.zeros((nsig * S, N), dtype=np.float32)
+    j = np.arange(N)
+    for row in range(nsig):
+        for s in range(S):
+            g = first + s
+            s0 = 2 * H * (g - 1) - origin
+            sh = N - H if g & 1 else H
+            jj = (j + sh) & (N - 1)
+            i = s0 + jj
+            ic = np.clip(i, 0, length - 1)
+            assert ic.min() >= 0 and ic.max() < length
+            a = sig[row, ic] * ((i >= 0) & (i < length)).astype(np.float32)
+            out[row * S + s] = win[jj] * a
+    return out
+
+
+def stream_overlap(y, tail, k):
+    """k_stream_overlap: y [nsig, N] one inverse slice k per signal; returns
+    (out or None, new tail)."""
+    H = N // 4
+    p = np.arange(2 * H)
+    sh = H if k & 1 else N - H
+    a = y[:, (p + sh) & (N - 1)]
+    b = y[:, (p + 2 * H + sh) & (N - 1)]
+    return (tail + a if k > 0 else None), b

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 5
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 6
 
 
 def test_status_strings(lib):
@@ -70,11 +70,17 @@ def test_argument_errors_detected_before_any_launch(lib):
     assert lib.fcqt_synthesis(ctypes.byref(tab), p, null, p, p, 0, p, p, p, 1, s) == EARG
     assert lib.fcqt_fill_zero(null, 10, s) == EARG
     # sliced framing entry points
-    assert lib.fcqt_slice_fft_fwd(ctypes.byref(tab), null, 100, p, 1, 1, p, p, s) == EARG
-    assert lib.fcqt_slice_fft_fwd(ctypes.byref(tab), p, 100, p, 1, 0, p, p, s) == EARG
-    assert lib.fcqt_route_bands_sliced(ctypes.byref(tab), p, null, p, p, 1, 1, s) == EARG
-    assert lib.fcqt_route_bands_sliced(ctypes.byref(tab), p, ctypes.c_void_p(4104), p, p, 1, 1, s) == EALIGN
-    assert lib.fcqt_scatter_bands_sliced(ctypes.byref(tab), p, p, p, null, 1, 1, s) == EARG
+    assert lib.fcqt_slice_fft_fwd(ctypes.byref(tab), null, 100, p, 1, 1, 0, 0, p, p, s) == EARG
+    assert lib.fcqt_slice_fft_fwd(ctypes.byref(tab), p, 100, p, 1, 0, 0, 0, p, p, s) == EARG
+    assert lib.fcqt_slice_fft_fwd(ctypes.byref(tab), p, 100, p, 1, 1, -1, 0, p, p, s) == EARG   # negative first
+    assert lib.fcqt_route_bands_sliced(ctypes.byref(tab), p, null, p, p, 1, 1, 0, s) == EARG
+    assert lib.fcqt_route_bands_sliced(ctypes.byref(tab), p, p, p, p, 1, 1, -3, s) == EARG
+    assert lib.fcqt_route_bands_sliced(ctypes.byref(tab), p, ctypes.c_void_p(4104), p, p, 1, 1, 0, s) == EALIGN
+    assert lib.fcqt_scatter_bands_sliced(ctypes.byref(tab), p, p, p, null, 1, 1, 0, s) == EARG
+    assert lib.fcqt_stream_overlap(p, null, p, 1, 1, s) == EARG                 # no tail
+    assert lib.fcqt_stream_overlap(p, p, null, 1, 2, s) == EARG                 # output needed after slice 0
+    assert lib.fcqt_stream_overlap(p, p, p, 0, 1, s) == EARG
+    assert lib.fcqt_stream_overlap(p, p, p, 1, -1, s) == EARG
     assert lib.fcqt_overlap_add(p, p, 1, 1, 2 * 32768 + 1, s) == EARG      # longer than nslices * 2H
     assert lib.fcqt_overlap_add(p, null, 1, 1, 10, s) == EARG
     assert lib.fcqt_fill_zero(p, 0, s) == 0  # nothing to do, no launch

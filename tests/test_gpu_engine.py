@@ -342,6 +342,43 @@ def test_sliced_stream_equals_whole_buffer():
     assert md < 1e-5 and rd < 1e-5
 
 
+def test_sliced_stream_fused_equals_host_framing():
+    """Streaming with the framing in the kernels (one fused call per slice,
+    the overlap-add carrying the tail) equals the host-framed stream bit for
+    bit, and equals the whole-buffer fused transform slice by slice."""
+    from flash_cqt import SlicedCQT
+    s = SlicedCQT(device=_dev())
+    rs = np.random.RandomState(9)
+    x = gpu(rs.standard_normal((2, 2, 3 * s.hop + 123)))
+    n = x.shape[-1]
+    S = s._num_slices(n)
+    xp = torch.cat([x, torch.zeros(2, 2, (S - 1) * s.hop - n, device=_dev())], dim=-1)
+    chunks = [xp[..., i * s.hop:(i + 1) * s.hop] for i in range(S - 1)]
+    res = {}
+    with torch.no_grad():
+        for fused in (True, False):
+            s.fused_framing = fused
+            sl = list(s.stream_fwd(iter(chunks)))
+            ys = list(s.stream_bwd(iter(sl)))
+            res[fused] = (sl, ys)
+        s.fused_framing = True
+        bl, sd = s.fwd(x)
+        yw = s.bwd(bl, sd)
+    (sf, yf), (sh, yh) = res[True], res[False]
+    assert len(sf) == len(sh) == S and len(yf) == len(yh) == S - 1
+    m = s.size_per_oct
+    for k in range(S):
+        for a, b in zip(sf[k][0] + sf[k][1], sh[k][0] + sh[k][1]):
+            assert a.shape == b.shape and torch.equal(a, b), k
+        for i, c in enumerate(sf[k][0]):
+            assert torch.equal(c, bl[i][..., k * m[i]:(k + 1) * m[i]]), (k, i)
+        for i, c in enumerate(sf[k][1]):
+            assert torch.equal(c, sd[i][:, :, k]), (k, i)
+    for a, b in zip(yf, yh):
+        assert torch.equal(a, b)
+    assert torch.equal(torch.cat(yf, dim=-1), yw[..., :(S - 1) * s.hop])
+
+
 def test_sliced_fused_framing_equals_engine_composition():
     """The fused framing (slices read from the signal, block-layout stores,
     overlap-add kernel) is bitwise the engine + torch-glue composition that

@@ -178,3 +178,49 @@ def test_reference_named_window_helpers_cpu():
                for d, od in zip(gd, b.gd))
     with pytest.raises(ValueError):
         R.nsdual(g, wins, nn)
+
+
+def test_sliced_framing_index_math_cpu():
+    """The sliced column pass's framing (whole signal, and one streamed slice
+    from [previous chunk, chunk] with first = k, origin = hop (k - 1)) equals
+    the reference framing: zero pad, 50% overlap, Tukey window, quarter roll."""
+    from oracle.cqt_oracle import makewnd
+    N, H = ks.N, ks.N // 4
+    hop = 2 * H
+    rs = np.random.RandomState(3)
+    win = makewnd(N, N // 4).astype(np.float32)
+    for length in (1, 1000, 3 * hop + 17, 5 * hop):
+        x = rs.standard_normal((2, length)).astype(np.float32)
+        quarters = -(-length // H)
+        S = (quarters + 1) // 2 + 1
+        xp = np.concatenate([np.zeros((2, 2 * H), np.float32), x,
+                             np.zeros((2, quarters * H - length + 3 * H), np.float32)], axis=1)
+        ref = np.stack([np.roll(xp[:, 2 * H * s:2 * H * s + N] * win, -H if s % 2 == 0 else H, axis=1)
+                        for s in range(S)], axis=1).reshape(2 * S, N)
+        assert np.array_equal(ks.sliced_frames(x, win, S), ref)
+        # streamed: chunks of hop samples, zero padded, one call per slice
+        xs = np.concatenate([x, np.zeros((2, (S - 1) * hop - length), np.float32)], axis=1)
+        chunks = [xs[:, i * hop:(i + 1) * hop] for i in range(S - 1)]
+        prev = np.zeros_like(chunks[0])
+        for k, chunk in enumerate(chunks + [np.zeros_like(chunks[0])]):
+            buf = np.concatenate([prev, chunk], axis=1)
+            got = ks.sliced_frames(buf, win, 1, first=k, origin=hop * (k - 1))
+            assert np.array_equal(got, ref.reshape(2, S, N)[:, k]), (length, k)
+            prev = chunk
+
+
+def test_stream_overlap_index_math_cpu():
+    """The streamed overlap-add kernel's indexing equals the reference's roll
+    by +H (even slices) / -H (odd) and half-slice overlap-add."""
+    import torch
+    N, H = ks.N, ks.N // 4
+    rs = np.random.RandomState(4)
+    tail_ref, tail = None, np.zeros((3, 2 * H), np.float32)
+    for k in range(4):
+        y = rs.standard_normal((3, N)).astype(np.float32)
+        yr = torch.roll(torch.from_numpy(y), H if k % 2 == 0 else -H, -1).numpy()
+        out, tail = ks.stream_overlap(y, tail, k)
+        if k > 0:
+            assert np.array_equal(out, tail_ref + yr[:, :2 * H])
+        tail_ref = yr[:, 2 * H:]
+        assert np.array_equal(tail, tail_ref)
