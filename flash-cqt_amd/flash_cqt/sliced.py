@@ -25,6 +25,8 @@ import math
 
 import torch
 
+from . import _native
+
 from .ref_util import hann_fft_order
 from .oct_cqt import OctCQT
 
@@ -261,16 +263,32 @@ class SlicedCQT:
     # kernel that carries the half-slice tail. Same values as the host
     # framing below, which runs when the engine cannot (autograd, torch engine).
 
+    def _stream_ptrs(self, f, nsig):
+        """Raw pointers of the one-slice buffers for nsig signals (the engine's
+        own, sized at allocation), so a streamed step is two C-ABI calls."""
+        cache = self.__dict__.setdefault("_stream_ptr_cache", {})
+        st = cache.get(nsig)
+        if st is None:
+            st = {k: v.data_ptr() for k, v in self._ws(f, nsig, 1).items()}
+            st["tw"] = self._tw32().data_ptr()
+            cache[nsig] = st
+        return st
+
     def _stream_slice_fused(self, f, prev, chunk, k):
         B, C, hop = chunk.shape
         nsig = B * C
-        buf = torch.cat([prev, chunk], dim=-1).reshape(nsig, 2 * hop).to(torch.float32).contiguous()
-        ws = self._ws(f, nsig, 1)
-        f.slice_fft(buf, self._tw32(), 1, ws["X"], ws["W"], first=k, origin=hop * (k - 1))
+        buf = torch.cat([prev, chunk], dim=-1)         # [B, C, N]: the slice's samples
+        if buf.dtype != torch.float32:
+            buf = buf.float()
+        st = self._stream_ptrs(f, nsig)
+        sh = _native.stream_handle(f.dev.index)
+        _native.check(f.lib.fcqt_slice_fft_fwd(f._ct, buf.data_ptr(), 2 * hop, st["tw"], nsig, 1, k, hop * (k - 1),
+                                               st["X"], st["W"], sh), "slice_fft_fwd")
         coef = torch.empty(nsig * f.ncoef, dtype=torch.complex64, device=f.dev)
-        f.route_bands_sliced(ws["X"], coef, nsig, 1, first=k)
+        _native.check(f.lib.fcqt_route_bands_sliced(f._ct, f._tp["route"], f._tp["slice_groups"], st["X"],
+                                                    coef.data_ptr(), nsig, 1, k, sh), "route_bands_sliced")
         ng = len(self.oct_bins)
-        views = [coef[nsig * off:nsig * (off + b * M)].view(B, C, b, M) for b, M, off in f.gspec]
+        views = [coef.as_strided((B, C, b, M), (C * b * M, b * M, M, 1), nsig * off) for b, M, off in f.gspec]
         return views[:ng], views[ng:]
 
     def _stream_slice_host(self, prev, chunk, k):
@@ -318,11 +336,17 @@ class SlicedCQT:
                 elif not (tail.is_contiguous() and tail.dtype == torch.float32 and tail.device == f.dev):
                     tail = tail.to(device=f.dev, dtype=torch.float32).contiguous()
                 coef = self._block_buffer(f, blocks, side, nsig, 1)
-                ws = self._ws(f, nsig, 1)
-                f.scatter_bands_sliced(coef, ws["F"], nsig, 1, first=k)
-                f.packed_ifft(ws["F"], ws["Y"], ws["W"])
+                st = self._stream_ptrs(f, nsig)
+                sh = _native.stream_handle(f.dev.index)
+                _native.check(f.lib.fcqt_scatter_bands_sliced(f._ct, f._tp["scat"], f._tp["slice_groups"],
+                                                              coef.data_ptr(), st["F"], nsig, 1, k, sh),
+                              "scatter_bands_sliced")
+                _native.check(f.lib.fcqt_packed_fft_inv(f._ct, f._tp["ovf_scat"], st["F"], st["Y"], st["W"], nsig,
+                                                        sh), "packed_fft_inv")
                 out = torch.empty(B, C, self.hop, dtype=torch.float32, device=f.dev) if k > 0 else None
-                f.stream_overlap(ws["Y"], tail, out, nsig, k)
+                _native.check(f.lib.fcqt_stream_overlap(st["Y"], tail.data_ptr(),
+                                                        out.data_ptr() if out is not None else None, nsig, k, sh),
+                              "stream_overlap")
                 if out is not None:
                     yield out
                 k += 1
