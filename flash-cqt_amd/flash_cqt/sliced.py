@@ -151,9 +151,16 @@ class SlicedCQT:
             return None
         return f
 
+    def _caches(self, f):
+        """Buffer caches of engine f; swapping self.cqt drops the old ones (the
+        slot buffer F belongs to one engine's scatter table)."""
+        if self.__dict__.get("_cache_owner") is not f:
+            self.__dict__.update(_cache_owner=f, _fused_ws={}, _stream_ptr_cache={})
+        return self.__dict__["_fused_ws"], self.__dict__["_stream_ptr_cache"]
+
     def _ws(self, f, nsig, S):
         """Engine buffers per (signals, slices per call); F is zeroed once."""
-        cache = self.__dict__.setdefault("_fused_ws", {})
+        cache = self._caches(f)[0]
         key = (nsig, S)
         if key not in cache:
             from . import tables as T
@@ -266,7 +273,7 @@ class SlicedCQT:
     def _stream_ptrs(self, f, nsig):
         """Raw pointers of the one-slice buffers for nsig signals (the engine's
         own, sized at allocation), so a streamed step is two C-ABI calls."""
-        cache = self.__dict__.setdefault("_stream_ptr_cache", {})
+        cache = self._caches(f)[1]
         st = cache.get(nsig)
         if st is None:
             st = {k: v.data_ptr() for k, v in self._ws(f, nsig, 1).items()}

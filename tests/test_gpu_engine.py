@@ -379,6 +379,24 @@ def test_sliced_stream_fused_equals_host_framing():
     assert torch.equal(torch.cat(yf, dim=-1), yw[..., :(S - 1) * s.hop])
 
 
+def test_sliced_engine_swap_rebuilds_buffers():
+    """Assigning a new engine to SlicedCQT.cqt drops the old engine's buffers;
+    whole-buffer and streamed results are unchanged."""
+    from flash_cqt import SlicedCQT
+    from flash_cqt.trainable import TrainableCQT
+    s = SlicedCQT(device=_dev())
+    x = gpu(np.random.RandomState(12).standard_normal((1, 1, 3 * s.hop)))
+    chunks = [x[..., i * s.hop:(i + 1) * s.hop] for i in range(3)]
+    with torch.no_grad():
+        y1 = s.bwd(*s.fwd(x))
+        z1 = torch.cat(list(s.stream_bwd(s.stream_fwd(iter(chunks)))), dim=-1)
+        s.cqt = TrainableCQT(s.oct, _dev())
+        y2 = s.bwd(*s.fwd(x))
+        z2 = torch.cat(list(s.stream_bwd(s.stream_fwd(iter(chunks)))), dim=-1)
+    assert torch.equal(y1, y2) and torch.equal(z1, z2)
+    assert s._cache_owner is s.cqt.f
+
+
 def test_sliced_fused_framing_equals_engine_composition():
     """The fused framing (slices read from the signal, block-layout stores,
     overlap-add kernel) is bitwise the engine + torch-glue composition that
