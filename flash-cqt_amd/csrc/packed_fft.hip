@@ -111,12 +111,21 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
     // every twiddle this thread needs, in flight with the data
     __shared__ float2 tw2[tw2_len<128>()];
     load_tw2_lds<128>(tw2, tws, threadIdx.x, 128);
+    // W_L^{n2 k1}, k1 = t + 8 q + 16 r, from the rows t, 8 and 16 r of the
+    // table: W^{n2 t} W^{8 n2 q} W^{16 n2 r} (two roundings more than a table value)
+    float2 tb = twp[t * 256 + n2], t8 = twp[8 * 256 + n2];
+    float2 t16[8];
+    t16[0] = make_float2(1.0f, 0.0f);
+#pragma unroll
+    for (int r = 1; r < 8; ++r) t16[r] = twp[16 * r * 256 + n2];
+    fft_unit<128, -1>(v, lds + c * P::US, t, tw2, Tw3<128>{});
+    const float2 tb8 = cmul(tb, t8);
     float2 tp[16];
 #pragma unroll
-    for (int q = 0; q < P::QL; ++q)
-#pragma unroll
-        for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + n2];
-    fft_unit<128, -1>(v, lds + c * P::US, t, tw2, Tw3<128>{});
+    for (int r = 0; r < 8; ++r) {
+        tp[r] = r ? cmul(tb, t16[r]) : tb;
+        tp[8 + r] = r ? cmul(tb8, t16[r]) : tb8;
+    }
     // v[q*8 + r] = V[k1], k1 = t + 8 q + 16 r
     float2* yb = out + (long)b * kL;
 #pragma unroll
@@ -161,10 +170,13 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
         q0[r] = fb[256 * (t + 8 * r) + col];
         q1[r] = fb[kFStride + 256 * (t + 8 * r) + col];
     }
-    // retangle and pass twiddles, in flight with the data
+    // retangle and pass twiddles, in flight with the data: W_N^{256 (t + 8 r) + col}
+    // = W_N^{256 t + col} W_N^{2048 r} (the second factor is the same for the
+    // whole workgroup), one rounding more than a table value
+    const float2 tnb = twn[256 * t + col];
     float2 tn[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) tn[r] = twn[256 * (t + 8 * r) + col];
+    for (int r = 0; r < 16; ++r) tn[r] = twn[2048 * r];
     __shared__ float2 tw2[tw2_len<128>()];
     load_tw2_lds<128>(tw2, tws, threadIdx.x, kInvThreads);
     float2 oadd = make_float2(0.0f, 0.0f);
@@ -210,16 +222,23 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
         // the factor 2 is removed by the 1/(2L) of the unpack
         const float2 sm = make_float2(f0.x + f1.x, f0.y - f1.y);
         const float2 d = make_float2(f0.x - f1.x, f0.y + f1.y);
-        const float2 o = cmulc(d, tn[r]);
+        const float2 o = cmulc(d, r ? cmul(tnb, tn[r]) : tnb);
         v[r] = make_float2(sm.x - o.y, -(sm.y + o.x));
     }
-    float2 tp[16];
+    const float2 pb = twp[t * 256 + col], p8 = twp[8 * 256 + col];
+    float2 p16[8];
+    p16[0] = make_float2(1.0f, 0.0f);
 #pragma unroll
-    for (int q = 0; q < P::QL; ++q)
-#pragma unroll
-        for (int r = 0; r < P::RL; ++r) tp[q * P::RL + r] = twp[(t + 8 * q + 16 * r) * 256 + col];
+    for (int r = 1; r < 8; ++r) p16[r] = twp[16 * r * 256 + col];
     __syncthreads();  // staged bins fully consumed before the FFT reuses LDS
     fft_unit<128, -1>(v, lds + c * P::US, t, tw2, Tw3<128>{});
+    const float2 pb8 = cmul(pb, p8);
+    float2 tp[16];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        tp[r] = r ? cmul(pb, p16[r]) : pb;
+        tp[8 + r] = r ? cmul(pb8, p16[r]) : pb8;
+    }
     float2* yb = out + (long)b * kL;
 #pragma unroll
     for (int q = 0; q < P::QL; ++q) {
