@@ -262,19 +262,22 @@ __device__ __forceinline__ int fwd_row(int w, int rho) {
 
 // Row FFTs of one 16-row tile, results left in LDS as Z_row[k2] at
 // lds[rho*US + pad16(k2)] (a barrier follows).
-// hold: values loaded before the call that must arrive with the row data
-// (the untangle twiddles), so they are not deferred past the barriers.
+// vhold / shold: a per-thread value and 16 workgroup-uniform values loaded
+// before the call that must arrive with the row data (the untangle
+// twiddles), so their loads are not deferred past the barriers.
 template <bool HOLD>
 __device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, float2* lds, float2* tw2,
-                                               int rho, int t, const float2* __restrict__ tws, float2* hold) {
+                                               int rho, int t, const float2* __restrict__ tws, float2* vhold,
+                                               float2* shold) {
     using P = Plan<256>;
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = yrow[t + 16 * r];
     load_tw2_lds<256>(tw2, tws, threadIdx.x, 256);
     if constexpr (HOLD) {
+        asm volatile("" : "+v"(vhold->x), "+v"(vhold->y));
 #pragma unroll
-        for (int u = 0; u < 16; ++u) asm volatile("" : "+v"(hold[u].x), "+v"(hold[u].y));
+        for (int u = 0; u < 16; ++u) asm volatile("" : "+s"(shold[u].x), "+s"(shold[u].y));
     }
     float2* s = lds + rho * P::US;
     fft_unit<256, -1>(v, s, t, tw2, Tw3<256>{});
@@ -295,14 +298,17 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
     const int w = lg - b * kRowWgs;
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
-    // untangle twiddles of this thread's output bins, loaded up front
+    // untangle twiddles of this thread's output bins, loaded up front:
+    // W_N^{k1 + 128 (kg + 16 u)} = W_N^{k1 + 128 kg} W_N^{2048 u}, the second
+    // factor the same for the whole workgroup (one rounding more than a table value)
     const int rho2 = threadIdx.x & 15;
     const int kg = threadIdx.x >> 4;
     const int k1 = fwd_row(w, rho2);
-    float2 wn[16];
+    float2 wb = twn[k1 + 128 * kg];
+    float2 wu[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) wn[u] = twn[k1 + 128 * (kg + 16 * u)];
-    row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, tw2, rho, t, tws, wn);
+    for (int u = 0; u < 16; ++u) wu[u] = twn[2048 * u];
+    row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, tw2, rho, t, tws, &wb, wu);
     // untangle: lanes walk the tile's rows for coalesced stores
     const float2* s = lds + rho2 * P::US;
     // mirror bin L - k: row 128 - k1 at column 255 - k2; rows 0 and 64 are
@@ -318,8 +324,9 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
         // X = E + W O,  E = (z + conj zm)/2,  O = (z - conj zm)/(2i),  W = W_N^k
         const float2 sm = make_float2(z.x + zm.x, z.y - zm.y);
         const float2 d = make_float2(z.x - zm.x, z.y + zm.y);
-        xb[k1 + 128 * k2] = make_float2(0.5f * fmaf(wn[u].x, d.y, fmaf(wn[u].y, d.x, sm.x)),
-                                        0.5f * fmaf(wn[u].y, d.y, fmaf(-wn[u].x, d.x, sm.y)));
+        const float2 wn = u ? cmul(wb, wu[u]) : wb;
+        xb[k1 + 128 * k2] = make_float2(0.5f * fmaf(wn.x, d.y, fmaf(wn.y, d.x, sm.x)),
+                                        0.5f * fmaf(wn.y, d.y, fmaf(-wn.x, d.x, sm.y)));
     }
     if (w == 0 && threadIdx.x == 0) {               // Nyquist bin from Z[0] (row 0, k2 = 0)
         const float2 z0 = lds[pad16(0)];
@@ -338,7 +345,7 @@ __global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, 
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
     row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, tw2, rho, t, tws,
-                          nullptr);
+                          nullptr, nullptr);
     const int rho2 = threadIdx.x & 15;
     const int kg = threadIdx.x >> 4;
     const float2* s2 = lds + rho2 * P::US;
