@@ -195,6 +195,23 @@ def test_round_trip_full_batch(fused, B):
     assert worst >= 125
 
 
+def test_large_odd_batch(fused):
+    """B = 301 (grids well past one round of workgroups, not a multiple of the
+    XCD count): every row round-trips, and rows equal their batch-1 results
+    bit for bit."""
+    B = 301
+    rs = np.random.RandomState(301)
+    x = rs.standard_normal((B, N)).astype(np.float32)
+    xg = gpu(x)
+    KR, KI = fused.fwd(xg)
+    k = torch.complex(KR, KI).clone()
+    y = cnp(fused.bwd(KR, KI))
+    assert min(snr_db(x[b], y[b]) for b in range(B)) >= 125
+    for b in (0, 150, 300):
+        k1, i1 = fused.fwd(xg[b:b + 1])
+        assert torch.equal(torch.complex(k1, i1)[0], k[b])
+
+
 def test_side_bands_dropped_like_oracle(train, oracle):
     x, _ = inputs()
     with torch.no_grad():
