@@ -254,12 +254,20 @@ __device__ __forceinline__ void load_tw3(Tw3<M>& w3, const float2* __restrict__ 
     if constexpr (R > 1) {
         static_assert(R == 2 || R == 4 || R == 8, "third-stage radix");
         constexpr int T = M / 16;
+        constexpr int Q = Tw3<M>::Q;
+        static_assert(T * Q == 256, "butterfly columns k = t + T q stay below 256");
+        // k = t + T q: the bases of butterfly q are those of q = 0 times
+        // W^{r T q}, the same for the whole workgroup (one rounding more
+        // than a table value)
+        const float2* blk = tws + tw_off(256, R);
+        w3.b[0][0] = blk[256 + t];
+        if constexpr (R >= 4) w3.b[0][1] = blk[512 + t];
+        if constexpr (R == 8) w3.b[0][2] = blk[1024 + t];
 #pragma unroll
-        for (int q = 0; q < Tw3<M>::Q; ++q) {
-            const float2* col = tws + tw_off(256, R) + ((t + T * q) & 255);
-            w3.b[q][0] = col[256];
-            if constexpr (R >= 4) w3.b[q][1] = col[512];
-            if constexpr (R == 8) w3.b[q][2] = col[1024];
+        for (int q = 1; q < Q; ++q) {
+            w3.b[q][0] = cmul(w3.b[0][0], blk[256 + T * q]);
+            if constexpr (R >= 4) w3.b[q][1] = cmul(w3.b[0][1], blk[512 + T * q]);
+            if constexpr (R == 8) w3.b[q][2] = cmul(w3.b[0][2], blk[1024 + T * q]);
         }
     }
 }
