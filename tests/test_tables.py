@@ -224,3 +224,24 @@ def test_stream_overlap_index_math_cpu():
             assert np.array_equal(out, tail_ref + yr[:, :2 * H])
         tail_ref = yr[:, 2 * H:]
         assert np.array_equal(tail, tail_ref)
+
+
+def test_sliced_block_buffer_detection_cpu():
+    """SlicedCQT.bwd reads the fused forward's coefficient buffer in place only
+    when handed that buffer's own group views; otherwise it assembles a copy
+    (zeros for missing side blocks)."""
+    import types
+    import torch
+    from flash_cqt.sliced import SlicedCQT
+    s = SlicedCQT.__new__(SlicedCQT)                     # host logic only
+    f = types.SimpleNamespace(gspec=[(2, 4, 0), (1, 8, 8), (1, 4, 16)], ncoef=20, dev=torch.device("cpu"))
+    nsig, S = 3, 2
+    coef = torch.arange(nsig * S * f.ncoef, dtype=torch.float32).to(torch.complex64)
+    views = [coef[nsig * S * off:nsig * S * (off + b * M)].view(1, nsig, b, S * M) for b, M, off in f.gspec]
+    blocks, side = views[:2], views[2:]
+    assert s._block_buffer(f, blocks, side, nsig, S) is coef
+    copy = s._block_buffer(f, [b.clone() for b in blocks], [c.clone() for c in side], nsig, S)
+    assert copy is not coef and torch.equal(copy, coef)
+    noside = s._block_buffer(f, blocks, None, nsig, S)
+    tail = nsig * S * 16
+    assert torch.equal(noside[:tail], coef[:tail]) and not noside[tail:].any()
