@@ -75,7 +75,6 @@ class SlicedCQT:
         else:
             self.cqt = oct_
         self.tw = makewnd(sl_len, tr_area, device=device, dtype=dtype)
-        self._roll = [m // 4 for m in self.size_per_oct]
         # run the framing inside the HIP engine's kernels when it can (False:
         # always frame on the host around self.cqt, as the reference does)
         self.fused_framing = True
@@ -107,32 +106,68 @@ class SlicedCQT:
         return "\n".join(lines)
 
     # ------------------------------------------------------------ slicing
+    # Host framing, written the way the sliced kernels read: index maps, not
+    # pad / unfold / roll. Slice g of a signal holds x[2H (g - 1) + jj] tw[jj]
+    # at position j, with jj = (j + H) mod N for even g and (j - H) mod N for
+    # odd g and zero outside the signal; the inverse un-rolls with the same
+    # maps and overlap-adds half slices. The values are the reference
+    # framing's bit for bit (sliced.py:106-166): every sample is one product
+    # x * tw, every overlap one sum of two half slices.
 
     def _num_slices(self, L):
         quarters = -(-L // self.H)
         return (quarters + 1) // 2 + 1
 
-    def _slice(self, x):
-        """[B, C, L] -> windowed, rolled slices [B, C, S, sl_len]."""
-        B, C, L = x.shape
-        H = self.H
-        S = self._num_slices(L)
-        quarters = -(-L // H)
-        xp = torch.cat([x.new_zeros(B, C, 2 * H), x,
-                        x.new_zeros(B, C, quarters * H - L + 3 * H)], dim=-1)
-        sl = xp.unfold(-1, 4 * H, 2 * H)[:, :, :S, :] * self.tw
-        even = (torch.arange(S, device=x.device) % 2 == 0).view(1, 1, -1, 1)
-        return torch.where(even, torch.roll(sl, -H, -1), torch.roll(sl, H, -1))
+    def _frame_maps(self, L, S, first, origin, device):
+        """(signal index clamped into [0, L), in-signal mask, window index jj),
+        each [S, N], for slices first .. first + S - 1 of a signal held from
+        sample `origin` on. Cached by what they depend on (the parity of
+        first and the start of slice `first` relative to the buffer)."""
+        N, H = self.sl_len, self.H
+        c0 = 2 * H * (first - 1) - origin
+        key = (L, S, first & 1, c0, str(device))
+        cache = self.__dict__.setdefault("_frame_cache", {})
+        if key not in cache:
+            g = torch.arange(first & 1, (first & 1) + S, device=device).view(-1, 1)
+            j = torch.arange(N, device=device).view(1, -1)
+            jj = (j + torch.where(g % 2 == 0, H, N - H)) % N
+            i = c0 + 2 * H * (g - (first & 1)) + jj
+            cache[key] = (i.clamp(0, L - 1), (i >= 0) & (i < L), jj)
+        return cache[key]
 
-    def _arrange(self, blocks, S, fwd):
-        """Undo (fwd) / redo (bwd) the quarter roll on the octave blocks;
-        side blocks stay rolled."""
+    def _slice(self, x, first=0, origin=0, S=None):
+        """[B, C, L] -> windowed, rolled slices [B, C, S, sl_len] (slices
+        first .. first + S - 1; x starts at signal sample `origin`)."""
+        L = x.shape[-1]
+        S = self._num_slices(L) if S is None else S
+        idx, inside, jj = self._frame_maps(L, S, first, origin, x.device)
+        taps = torch.where(inside, x[..., idx], x.new_zeros(()))
+        return taps * self.tw[jj]
+
+    def _quarter_roll(self, blocks, first, fwd):
+        """Octave blocks [..., S, bins, M] between transform order and the
+        layout fwd returns: transform output m of slice g sits at
+        (m + M/4) mod M for even g and (m - M/4) mod M for odd g (fwd=True
+        applies that, fwd=False undoes it). Side blocks are not rolled."""
         out = []
-        sgn = 1 if fwd else -1
-        for c, r in zip(blocks, self._roll):
-            even = (torch.arange(S, device=c.device) % 2 == 0).view(1, 1, -1, 1, 1)
-            out.append(torch.where(even, torch.roll(c, sgn * r, -1), torch.roll(c, -sgn * r, -1)))
+        for c in blocks:
+            S, M = c.shape[-3], c.shape[-1]
+            g = torch.arange(first, first + S, device=c.device).view(-1, 1, 1)
+            shift = torch.where(g % 2 == 0, M // 4, M - M // 4)
+            m = torch.arange(M, device=c.device).view(1, 1, -1)
+            src = (m - shift) % M if fwd else (m + shift) % M
+            out.append(torch.take_along_dim(c, src.view((1,) * (c.dim() - 3) + tuple(src.shape)), dim=-1))
         return out
+
+    def _unroll_slices(self, y, first):
+        """Inverse slices [..., S, N] back from the quarter roll: even g by +H,
+        odd g by -H (position j takes y[(j -+ H) mod N])."""
+        N, H = self.sl_len, self.H
+        S = y.shape[-2]
+        g = torch.arange(first, first + S, device=y.device).view(-1, 1)
+        j = torch.arange(N, device=y.device).view(1, -1)
+        src = (j + torch.where(g % 2 == 0, N - H, H)) % N
+        return torch.take_along_dim(y, src.view((1,) * (y.dim() - 2) + tuple(src.shape)), dim=-1)
 
     # ------------------------------------------- fused framing (HIP engine)
 
@@ -237,8 +272,9 @@ class SlicedCQT:
         sl = self._slice(x)
         S = sl.shape[2]
         blocks, side = self.cqt.fwd(sl)
-        blocks = self._arrange(blocks, S, fwd=True)
-        blocks = [c.permute(0, 1, 3, 2, 4).reshape(B, C, b, S * m)
+        blocks = self._quarter_roll(blocks, 0, fwd=True)
+        # [B, C, S, bins, M] -> [B, C, bins, S M]: slices in time order per band
+        blocks = [c.transpose(2, 3).reshape(B, C, b, S * m)
                   for c, b, m in zip(blocks, self.oct_bins, self.size_per_oct)]
         return blocks, side
 
@@ -249,17 +285,17 @@ class SlicedCQT:
             return self._bwd_fused(f, blocks, side, length)
         B, C = blocks[0].shape[:2]
         S = blocks[0].shape[-1] // self.size_per_oct[0]
-        blocks = [c.reshape(B, C, b, S, m).permute(0, 1, 3, 2, 4)
+        blocks = [c.reshape(B, C, b, S, m).transpose(2, 3)
                   for c, b, m in zip(blocks, self.oct_bins, self.size_per_oct)]
-        blocks = self._arrange(blocks, S, fwd=False)
-        y = self.cqt.bwd(blocks, side)
-        H = self.H
-        even = (torch.arange(S, device=y.device) % 2 == 0).view(1, 1, -1, 1)
-        y = torch.where(even, torch.roll(y, H, -1), torch.roll(y, -H, -1))
-        out = y.new_zeros(B, C, (S + 1) * 2 * H)
-        out[..., :S * 2 * H] += y[..., :2 * H].reshape(B, C, -1)
-        out[..., 2 * H:] += y[..., 2 * H:].reshape(B, C, -1)
-        out = out[..., 2 * H:]
+        blocks = self._quarter_roll(blocks, 0, fwd=False)
+        y = self._unroll_slices(self.cqt.bwd(blocks, side), 0)
+        # output hop t (2H samples, from signal sample 2H (t - 1)) is the first
+        # half of slice t plus the second half of slice t - 1; hop 0 lies in
+        # the leading padding and is dropped
+        hops = y.reshape(B, C, S, 2, 2 * self.H)
+        pad = torch.nn.functional.pad
+        out = (pad(hops[..., 0, :], (0, 0, 0, 1)) + pad(hops[..., 1, :], (0, 0, 1, 0)))[..., 1:, :]
+        out = out.reshape(B, C, S * 2 * self.H)
         return out[..., :length] if length is not None else out
 
     # --------------------------------------------- streaming, bounded state
@@ -299,11 +335,10 @@ class SlicedCQT:
         return views[:ng], views[ng:]
 
     def _stream_slice_host(self, prev, chunk, k):
-        sl = torch.cat([prev, chunk], dim=-1) * self.tw
-        sl = torch.roll(sl, -self.H if k % 2 == 0 else self.H, -1)
-        blocks, side = self.cqt.fwd(sl.unsqueeze(2))
-        # a single slice is "even" for _arrange; odd slices roll the other way
-        blocks = self._arrange(blocks, 1, fwd=(k % 2 == 0))
+        hop = chunk.shape[-1]
+        sl = self._slice(torch.cat([prev, chunk], dim=-1), first=k, origin=hop * (k - 1), S=1)
+        blocks, side = self.cqt.fwd(sl)
+        blocks = self._quarter_roll(blocks, k, fwd=True)
         return [c[:, :, 0] for c in blocks], [c[:, :, 0] for c in side]
 
     def stream_fwd(self, chunks):
@@ -358,11 +393,9 @@ class SlicedCQT:
                     yield out
                 k += 1
                 continue
-            blocks = [c.unsqueeze(2) for c in blocks]
+            blocks = self._quarter_roll([c.unsqueeze(2) for c in blocks], k, fwd=False)
             side = [c.unsqueeze(2) for c in side] if side is not None else None
-            blocks = self._arrange(blocks, 1, fwd=(k % 2 != 0))
-            y = self.cqt.bwd(blocks, side)[:, :, 0]
-            y = torch.roll(y, self.H if k % 2 == 0 else -self.H, -1)
+            y = self._unroll_slices(self.cqt.bwd(blocks, side), k)[:, :, 0]
             if k > 0:
                 yield tail + y[..., :self.hop]
             tail = y[..., self.hop:]

@@ -245,3 +245,50 @@ def test_sliced_block_buffer_detection_cpu():
     noside = s._block_buffer(f, blocks, None, nsig, S)
     tail = nsig * S * 16
     assert torch.equal(noside[:tail], coef[:tail]) and not noside[tail:].any()
+
+
+def test_product_sliced_host_framing_matches_reference_cpu(golden):
+    """flash_cqt.SlicedCQT with the torch engine on the CPU (the host framing
+    that autograd and the torch engine use) against the reference's own
+    SlicedCQT vectors, and its stream against its whole-buffer transform."""
+    import hashlib
+    import torch
+    from golden.golden_inputs import sliced_input
+    from flash_cqt import SlicedCQT
+    s = SlicedCQT(engine="torch")
+    x = torch.from_numpy(sliced_input())
+    with torch.no_grad():
+        bl, sd = s.fwd(x)
+        y = s.bwd(bl, sd, length=x.shape[-1])
+    st = int(golden["meta_stride"][0])
+    sts = int(golden["meta_stride"][1])
+    assert [list(c.shape) for c in bl] == golden["sliced_shapes"].tolist()
+    tw = s.tw.numpy().astype(np.float32)
+    assert hashlib.sha256(np.ascontiguousarray(tw).tobytes()).hexdigest() == golden["sliced_tw_sha256"][0]
+    cb = np.concatenate([c.numpy().reshape(1, 2, -1)[..., ::sts] for c in bl], -1)
+    cs = np.concatenate([c.numpy().reshape(1, 2, -1)[..., ::st] for c in sd], -1)
+    assert snr_db(golden["sliced_blocks_sub"], cb) > 120
+    assert snr_db(golden["sliced_side_sub"], cs) > 120
+    assert snr_db(golden["sliced_bwd_sub"], y.numpy()[..., ::st]) > 120
+    # streamed (hop chunks, bounded state): each streamed slice is framed bit
+    # for bit as the whole buffer frames it, and the stream reproduces the
+    # whole-buffer transform (to the torch engine's batch-size rounding)
+    n = x.shape[-1]
+    S = s._num_slices(n)
+    xp = torch.cat([x, torch.zeros(*x.shape[:2], (S - 1) * s.hop - n)], dim=-1)
+    chunks = [xp[..., i * s.hop:(i + 1) * s.hop] for i in range(S - 1)]
+    whole = s._slice(x)
+    prev = torch.zeros_like(chunks[0])
+    for k, chunk in enumerate(chunks + [torch.zeros_like(chunks[0])]):
+        one = s._slice(torch.cat([prev, chunk], dim=-1), first=k, origin=s.hop * (k - 1), S=1)
+        assert torch.equal(one, whole[:, :, k:k + 1])
+        prev = chunk
+    with torch.no_grad():
+        out = list(s.stream_fwd(iter(chunks)))
+        ys = torch.cat(list(s.stream_bwd(iter(out))), dim=-1)
+        yfull = s.bwd(bl, sd)
+    m = s.size_per_oct
+    for k, (blk, side) in enumerate(out):
+        for i, c in enumerate(blk):
+            assert snr_db(bl[i][..., k * m[i]:(k + 1) * m[i]].numpy(), c.numpy()) > 120
+    assert snr_db(yfull[..., :ys.shape[-1]].numpy(), ys.numpy()) > 125
