@@ -86,15 +86,16 @@ class SlicedCQT:
         return 1000.0 * (sl_len if sl_len is not None else self.sl_len) / self.fs
 
     def lowest_fmin(self, sl_len=None):
-        """Lowest fmin whose analysis window still fits a slice (sl_len >= 8 fs q / f)."""
-        sl = sl_len if sl_len is not None else self.sl_len
-        n0 = 1
-        while n0 < len(self.oct_bins) and self.oct_bins[n0] == self.oct_bins[0]:
-            n0 += 1
-        b0 = self.oct_bins[0]
-        step = 2.0 ** ((n0 + 1) / ((n0 + 1) * b0 - 1))
-        q0 = math.sqrt(step) / (step - 1.0) / 2.0
-        return 8.0 * self.fs * q0 / sl
+        """Lowest analysis frequency a slice of sl_len samples still holds a
+        full window for. A window at frequency f spans 8 fs Q / f samples, so
+        f >= 8 fs Q / sl_len, where Q is the quality factor of the lowest bin
+        group: that group spans its n octaves plus the dropped one below in
+        (n + 1) b - 1 geometric steps of ratio r, and Q = sqrt(r) / (r - 1) / 2."""
+        sl = self.sl_len if sl_len is None else sl_len
+        b = self.oct_bins[0]
+        n = next((i for i, v in enumerate(self.oct_bins) if v != b), len(self.oct_bins))
+        r = 2.0 ** ((n + 1) / ((n + 1) * b - 1))
+        return 8.0 * self.fs * (math.sqrt(r) / (r - 1.0) / 2.0) / sl
 
     def latency_table(self, sl_lens=(8192, 16384, 32768, 65536, 131072)):
         need = float(self.frqs_hz[0])
