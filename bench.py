@@ -274,7 +274,7 @@ def cpu_baseline(batch=64, budget_s=10.0, budget_b1_s=4.0, max_reps=400):
     """The reference OctCQT algorithm (oracle torch port) on the host cores,
     on a bounded sample of the bench's own workload (batch-`batch` round trips
     of the randn input, about budget_s of CPU work), plus batch 1 on the
-    configs[1] input."""
+    configs[1] input and batches 4 and 16 on randn input (short samples)."""
     from oracle.torch_port import TorchPortOctCQT
     cores = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(cores)
@@ -294,6 +294,12 @@ def cpu_baseline(batch=64, budget_s=10.0, budget_b1_s=4.0, max_reps=400):
 
     med, n, db = timed(randn(batch, 0), budget_s)
     med1, n1, db1 = timed(torch.from_numpy(sinusoids()), budget_b1_s)
+    per_batch = {"1": {"round_trips_per_s": 1.0 / med1, "median_ms": med1 * 1e3, "reps": n1},
+                 str(batch): {"round_trips_per_s": batch / med, "median_ms": med * 1e3, "reps": n}}
+    for b in (4, 16):
+        if str(b) not in per_batch:
+            mb, nb, _ = timed(randn(b, 0), budget_b1_s / 2)
+            per_batch[str(b)] = {"round_trips_per_s": b / mb, "median_ms": mb * 1e3, "reps": nb}
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -308,7 +314,8 @@ def cpu_baseline(batch=64, budget_s=10.0, budget_b1_s=4.0, max_reps=400):
                       f"per batch), oracle/torch_port.py, torch CPU {cores} threads, {model}",
             "snr_db": db,
             "batch1": {"value": 1.0 / med1, "sample": f"{n1} batch-1 round trips of the configs[1] input "
-                                                     f"(median {med1 * 1e3:.2f} ms)", "snr_db": db1}}
+                                                     f"(median {med1 * 1e3:.2f} ms)", "snr_db": db1},
+            "per_batch": per_batch}
 
 
 # ---------------------------------------------------------- kernel timings
