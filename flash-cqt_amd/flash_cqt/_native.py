@@ -93,13 +93,24 @@ def ptr(t):
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
 
 
 def stream_handle(device_index=None):
     """hipStream_t (as an int) of the current torch stream of a device
-    (default: the current device)."""
+    (default: the current device).
+
+    The device must be the current one: a launch on the default stream
+    (handle 0) goes to the current device, so an engine on another device
+    would otherwise be handed the wrong device's stream. Like a torch op
+    without a device guard, the caller selects the device
+    (torch.cuda.device / set_device); this raises instead of launching."""
+    cur = _get_device() if _get_device is not None else torch.cuda.current_device()
     if device_index is None:
-        device_index = torch.cuda.current_device()
+        device_index = cur
+    elif device_index != cur:
+        raise NativeError(f"engine is on cuda:{device_index} but the current device is cuda:{cur}; "
+                          f"launch under torch.cuda.device({device_index})")
     if _raw_stream is not None:
         return _raw_stream(device_index)
     return torch.cuda.current_stream(device_index).cuda_stream

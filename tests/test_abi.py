@@ -94,6 +94,18 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         _native.load()
 
 
+def test_stream_of_another_device_is_refused(monkeypatch):
+    """An engine on a device other than the current one gets an error, not
+    the current device's stream (the default stream launches there)."""
+    from flash_cqt import _native
+    monkeypatch.setattr(_native, "_get_device", lambda: 1)
+    monkeypatch.setattr(_native, "_raw_stream", lambda i: 1000 + i)
+    assert _native.stream_handle(1) == 1001
+    assert _native.stream_handle() == 1001
+    with pytest.raises(_native.NativeError, match="current device is cuda:1"):
+        _native.stream_handle(0)
+
+
 def test_engine_refuses_cpu_device(pkg_cqt_cpu):
     from flash_cqt.fused import FusedOctCQT
     with pytest.raises(ValueError):

@@ -321,6 +321,8 @@ def test_graph_replay_rebuilds_poisoned_outputs(fused):
         assert torch.equal(torch.complex(w["KR"], w["KI"]), eager_k)
         assert torch.equal(out, eager_y)
         _ = torch.randn(1000, device=_dev()).sum()  # eager work between replays
+    with pytest.raises(ValueError, match="shape"):
+        g(xg[:1])          # a [1, N] input is refused, not broadcast into [2, N]
 
 
 # -------------------------------------------------------------- sliced

@@ -292,3 +292,16 @@ def test_product_sliced_host_framing_matches_reference_cpu(golden):
         for i, c in enumerate(blk):
             assert snr_db(bl[i][..., k * m[i]:(k + 1) * m[i]].numpy(), c.numpy()) > 120
     assert snr_db(yfull[..., :ys.shape[-1]].numpy(), ys.numpy()) > 125
+
+
+def test_graphed_input_check_cpu():
+    """Graphed refuses a call whose inputs differ in count or shape from the
+    recorded ones (copy_ would otherwise broadcast a [1, N] input into a
+    recorded [4, N] buffer)."""
+    from flash_cqt.graphed import _check_inputs, _leaves
+    rec = list(_leaves((torch.zeros(4, 8), [torch.zeros(3)])))
+    _check_inputs(rec, list(_leaves((torch.ones(4, 8), [torch.ones(3)]))))
+    with pytest.raises(ValueError, match="shape"):
+        _check_inputs(rec, list(_leaves((torch.ones(1, 8), [torch.ones(3)]))))
+    with pytest.raises(ValueError, match="input tensors"):
+        _check_inputs(rec, list(_leaves((torch.ones(4, 8),))))
