@@ -212,6 +212,69 @@ def test_large_odd_batch(fused):
         assert torch.equal(torch.complex(k1, i1)[0], k[b])
 
 
+# ------------------------------------ size-independent properties at B = 64
+
+def test_power_of_two_scaling_bitwise(fused):
+    """Every operation on the path is linear in the data (sums, and products
+    of data with fixed twiddles, weights and gains; no data x data product),
+    so a power-of-two scale commutes with every rounding: fwd(4 x) = 4 fwd(x)
+    and bwd(K / 8) = bwd(K) / 8 bit for bit at the headline batch. A
+    data-dependent branch, stale workspace state or a reassociation between
+    the two runs would break the equality."""
+    B = 64
+    rs = np.random.RandomState(64064)
+    x = gpu(rs.standard_normal((B, N)).astype(np.float32))
+    KR, KI = fused.fwd(x)
+    k = torch.complex(KR, KI).clone()
+    y = fused.bwd(KR, KI).clone()
+    KR4, KI4 = fused.fwd(x * 4)
+    assert torch.equal(torch.complex(KR4, KI4), k * 4)
+    y8 = fused.bwd((k.real / 8).contiguous(), (k.imag / 8).contiguous())
+    assert torch.equal(y8, y / 8)
+
+
+def test_zero_input_gives_exact_zeros_after_nonzero_call(fused):
+    """No state survives between calls: after a random batch, a zero batch of
+    the same size gives exactly zero coefficients and exactly zero output."""
+    B = 4
+    rs = np.random.RandomState(4)
+    fused.bwd(*fused.fwd(gpu(rs.standard_normal((B, N)).astype(np.float32))))
+    KR, KI = fused.fwd(torch.zeros(B, N, device=_dev()))
+    assert not KR.any() and not KI.any()
+    y = fused.bwd(KR, KI)
+    assert not y.any()
+
+
+def test_linearity_full_batch(fused):
+    """fwd(a x + b z) = a fwd(x) + b fwd(z) and the same for bwd, to rounding
+    (>= 120 dB), at B = 64."""
+    B = 64
+    rs = np.random.RandomState(6464)
+    x = gpu(rs.standard_normal((B, N)).astype(np.float32))
+    z = gpu(rs.standard_normal((B, N)).astype(np.float32))
+    a, b = 0.37, -1.9
+
+    def k_of(v):
+        kr, ki = fused.fwd(v)
+        return torch.complex(kr, ki).clone()
+
+    kx, kz, ks = k_of(x), k_of(z), k_of(a * x + b * z)
+    assert snr_db(cnp(a * kx + b * kz), cnp(ks)) >= 120
+    y_sum = fused.bwd((a * kx + b * kz).real.contiguous(), (a * kx + b * kz).imag.contiguous()).clone()
+    yx = fused.bwd(kx.real.contiguous(), kx.imag.contiguous()).clone()
+    yz = fused.bwd(kz.real.contiguous(), kz.imag.contiguous()).clone()
+    assert snr_db(cnp(a * yx + b * yz), cnp(y_sum)) >= 120
+
+
+def test_synthesis_batch_independent_bitwise(fused):
+    rs = np.random.RandomState(1616)
+    C = (rs.standard_normal((16, fused.ncoef)) + 1j * rs.standard_normal((16, fused.ncoef))).astype(np.complex64)
+    y = fused.bwd(gpu(C.real), gpu(C.imag)).clone()
+    for b in (0, 7, 15):
+        y1 = fused.bwd(gpu(C.real[b:b + 1]), gpu(C.imag[b:b + 1]))
+        assert torch.equal(y1[0], y[b])
+
+
 def test_side_bands_dropped_like_oracle(train, oracle):
     x, _ = inputs()
     with torch.no_grad():
