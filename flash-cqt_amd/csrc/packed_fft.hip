@@ -29,13 +29,22 @@
 
 namespace fcqt {
 
-constexpr int kColsPerWg = 16;                 // column pass: 16 columns x 128 rows
-constexpr int kRowsPerWg = 16;                 // row pass: 16 rows x 256 columns
-constexpr int kColWgs = 256 / kColsPerWg;      // 16 workgroups per slice
-constexpr int kInvColsPerWg = 32;              // inverse column pass: 16 columns + 16 mirrors
-constexpr int kInvWgs = 256 / kInvColsPerWg;   // 8 workgroups per slice
-constexpr int kInvThreads = 8 * kInvColsPerWg;
-constexpr int kRowWgs = 128 / kRowsPerWg;      // 8 workgroups per slice
+// Tile shapes of the four pass kernels. Each kernel comes in a wide shape
+// (every tile row reads and writes whole 128-byte lines) and a narrow one
+// with half the columns or rows per workgroup and twice the workgroups per
+// slice. A small batch has few workgroups per pass (8-16 per slice), so its
+// pass time is set by what each workgroup moves; the narrow shapes halve
+// that. Large batches fill the chip either way and keep the wide shapes.
+//   column pass:          CPW columns x 128 rows, 8 CPW threads
+//   row passes:           RPW rows x 256 columns, 16 RPW threads
+//   inverse column pass:  CPW/2 columns + their CPW/2 mirrors, 8 CPW threads
+constexpr int kColsWide = 16, kColsNarrow = 8;
+constexpr int kRowsWide = 16, kRowsNarrow = 8;
+constexpr int kInvColsWide = 32, kInvColsNarrow = 16;
+// batch sizes up to this one run the narrow shapes
+constexpr int64_t kNarrowMaxBatch = 16;
+// the fold lists are built for the wide inverse column workgroups
+constexpr int kFoldLists = 256 / kInvColsWide;
 
 // ------------------------------------------------------------ column pass
 
@@ -81,18 +90,19 @@ __device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const float* 
     return make_float2(p0, p1);
 }
 
-template <bool SLICED>
-__global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, float2* __restrict__ out,
-                                                 const float2* __restrict__ twp,
-                                                 const float2* __restrict__ tws, const SliceSrc src) {
+template <bool SLICED, int CPW>
+__global__ __launch_bounds__(8 * CPW) void k_col_fwd(const float2* __restrict__ in, float2* __restrict__ out,
+                                                     const float2* __restrict__ twp,
+                                                     const float2* __restrict__ tws, const SliceSrc src) {
     using P = Plan<128>;
-    __shared__ float2 lds[kColsPerWg * P::US];
+    constexpr int kWgs = 256 / CPW;               // workgroups per slice
+    __shared__ float2 lds[CPW * P::US];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int b = lg / kColWgs;
-    const int cg = lg - b * kColWgs;
-    const int c = threadIdx.x & (kColsPerWg - 1);  // column within the tile
-    const int t = threadIdx.x >> 4;                // thread within the column FFT, < 8
-    const int n2 = cg * kColsPerWg + c;
+    const int b = lg / kWgs;
+    const int cg = lg - b * kWgs;
+    const int c = threadIdx.x & (CPW - 1);        // column within the tile
+    const int t = threadIdx.x / CPW;              // thread within the column FFT, < 8
+    const int n2 = cg * CPW + c;
     float2 v[16];
     if constexpr (SLICED) {
         const int sig = b / src.S;
@@ -110,7 +120,7 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
     }
     // every twiddle this thread needs, in flight with the data
     __shared__ float2 tw2[tw2_len<128>()];
-    load_tw2_lds<128>(tw2, tws, threadIdx.x, 128);
+    load_tw2_lds<128>(tw2, tws, threadIdx.x, 8 * CPW);
     // W_L^{n2 k1}, k1 = t + 8 q + 16 r, from the rows t, 8 and 16 r of the
     // table: W^{n2 t} W^{8 n2 q} W^{16 n2 r} (two roundings more than a table value)
     float2 tb = twp[t * 256 + n2], t8 = twp[8 * 256 + n2];
@@ -138,32 +148,45 @@ __global__ __launch_bounds__(128) void k_col_fwd(const float2* __restrict__ in, 
     }
 }
 
-// Column of local slot c in inverse column workgroup w: slots 0-15 hold
-// columns p = 16w..16w+15, slots 16-31 their mirrors 256 - p; pair p = 0 is
-// {0, 128} (both self-mirrored). Each half is 16 consecutive columns, so
-// every row of the tile reads and writes whole 128-byte lines.
+// Column of local slot c in inverse column workgroup w with H = CPW / 2
+// column pairs: slots 0..H-1 hold columns p = H w .. H w + H - 1, slots
+// H..2H-1 their mirrors 256 - p; pair p = 0 is {0, 128} (both
+// self-mirrored). Each half is H consecutive columns (whole 128-byte lines
+// per tile row in the wide shape, H = 16).
+template <int CPW>
 __device__ __forceinline__ int inv_col(int w, int c) {
-    const int p = 16 * w + (c & 15);
-    return c < 16 ? p : (p == 0 ? 128 : 256 - p);
+    constexpr int H = CPW / 2;
+    const int p = H * w + (c & (H - 1));
+    return c < H ? p : (p == 0 ? 128 : 256 - p);
 }
 
-__global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restrict__ f, float2* __restrict__ out,
-                                                         const float2* __restrict__ twp,
-                                                         const float2* __restrict__ twn,
-                                                         const int* __restrict__ fold,
-                                                         const float2* __restrict__ tws) {
+template <int CPW>
+__global__ __launch_bounds__(8 * CPW) void k_col_inv(const float2* __restrict__ f, float2* __restrict__ out,
+                                                     const float2* __restrict__ twp,
+                                                     const float2* __restrict__ twn,
+                                                     const int* __restrict__ fold,
+                                                     const float2* __restrict__ tws) {
     using P = Plan<128>;
-    __shared__ float2 lds[kInvColsPerWg * P::US];  // staged bins, then FFT exchange
+    constexpr int H = CPW / 2;                    // column pairs per workgroup
+    constexpr int kWgs = 256 / CPW;               // workgroups per slice
+    constexpr int kThreads = 8 * CPW;
+    constexpr int kShare = kWgs / kFoldLists;     // workgroups sharing one fold list
+    constexpr int kEnt = kFoldPerWg / kThreads;   // fold-list entries per thread
+    static_assert(kShare * kFoldLists == kWgs && kEnt * kThreads == kFoldPerWg, "fold list split");
+    __shared__ float2 lds[CPW * P::US];           // staged bins, then FFT exchange
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int b = lg / kInvWgs;
-    const int w = lg - b * kInvWgs;
-    const int c = threadIdx.x & (kInvColsPerWg - 1);
-    const int t = threadIdx.x >> 5;
-    const int col = inv_col(w, c);
+    const int b = lg / kWgs;
+    const int w = lg - b * kWgs;
+    const int c = threadIdx.x & (CPW - 1);
+    const int t = threadIdx.x / CPW;
+    const int col = inv_col<CPW>(w, c);
     const float2* fb = f + (long)b * kFRow;
     float2* raw = lds + c * P::US;
-    // fold list entry of this thread: bin | overflow index << 16, or -1
-    const int ent = fold[w * kFoldPerWg + threadIdx.x];
+    // fold list entries of this thread (bin | overflow index << 16, or -1),
+    // from the list of the wide workgroup that contains this one
+    int ent[kEnt];
+#pragma unroll
+    for (int e = 0; e < kEnt; ++e) ent[e] = fold[(w / kShare) * kFoldPerWg + threadIdx.x + e * kThreads];
     float2 q0[16], q1[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -178,21 +201,32 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
 #pragma unroll
     for (int r = 0; r < 16; ++r) tn[r] = twn[2048 * r];
     __shared__ float2 tw2[tw2_len<128>()];
-    load_tw2_lds<128>(tw2, tws, threadIdx.x, kInvThreads);
-    float2 oadd = make_float2(0.0f, 0.0f);
-    int opos = -1;
-    if (ent >= 0) {
-        const int bin = ent & 0xffff;
-        const int k = min(ent >> 16, kOvfCap - 1);
-        const float2* o = fb + 2 * kFStride + 2 * k;
-        oadd = cadd(o[0], o[1]);
-        if (bin >= kL) {
-            opos = 128;                          // column 0's pad slot holds bin L
-        } else {
-            const int cl = bin & 255, n1 = bin >> 8;
-            const int pp = cl <= 128 ? (cl == 128 ? 0 : cl) : 256 - cl;
-            const int cc = (cl < 128 ? 0 : 16) + (pp & 15);
-            opos = cc * P::US + n1;
+    load_tw2_lds<128>(tw2, tws, threadIdx.x, kThreads);
+    // overflow slot sums of this workgroup's listed bins and their LDS
+    // positions (bin L is parked in column 0's pad slot, raw[128] of slot 0)
+    float2 oadd[kEnt];
+    int opos[kEnt];
+#pragma unroll
+    for (int e = 0; e < kEnt; ++e) {
+        oadd[e] = make_float2(0.0f, 0.0f);
+        opos[e] = -1;
+        if (ent[e] >= 0) {
+            const int bin = ent[e] & 0xffff;
+            int pos = -1;
+            if (bin >= kL) {
+                if (w == 0) pos = 128;
+            } else {
+                const int cl = bin & 255, n1 = bin >> 8;
+                const int pp = cl <= 128 ? (cl == 128 ? 0 : cl) : 256 - cl;
+                if (pp / H == w)               // a bin of this workgroup's columns
+                    pos = ((cl < 128 ? 0 : H) + (pp & (H - 1))) * P::US + n1;
+            }
+            if (pos >= 0) {
+                const int k = min(ent[e] >> 16, kOvfCap - 1);
+                const float2* o = fb + 2 * kFStride + 2 * k;
+                oadd[e] = cadd(o[0], o[1]);
+                opos[e] = pos;
+            }
         }
     }
 #pragma unroll
@@ -201,7 +235,9 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
     // workgroup 0)
     if (col == 0 && t == 0) raw[128] = dense_bin(fb, kL);
     __syncthreads();
-    if (opos >= 0) lds[opos] = cadd(lds[opos], oadd);   // each listed bin appears once
+#pragma unroll
+    for (int e = 0; e < kEnt; ++e)
+        if (opos[e] >= 0) lds[opos[e]] = cadd(lds[opos[e]], oadd[e]);   // each listed bin appears once
     __syncthreads();
     if (col == 0 && t == 0) {          // bins 0 and L are real for irfft (after any fold)
         raw[0].y = 0.0f;
@@ -210,7 +246,7 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
     __syncthreads();
     // mirror bin L - i: column 256 - col at row 127 - n1; columns 0 and 128
     // are their own mirrors (column 0 at row 128 - n1, row 128 = bin L)
-    const float2* mp = (col == 0 || col == 128) ? raw : lds + (c ^ 16) * P::US;
+    const float2* mp = (col == 0 || col == 128) ? raw : lds + (c ^ H) * P::US;
     const int moff = col == 0 ? 128 : 127;
     float2 v[16];
 #pragma unroll
@@ -252,28 +288,31 @@ __global__ __launch_bounds__(kInvThreads) void k_col_inv(const float2* __restric
 
 // --------------------------------------------------------------- row pass
 
-// Row of local slot rho in forward row workgroup w: slots 0-7 hold rows
-// p = 8w..8w+7, slots 8-15 their mirrors 128 - p; pair p = 0 is {0, 64}
-// (both self-mirrored).
+// Row of local slot rho in forward row workgroup w with HP = RPW / 2 row
+// pairs: slots 0..HP-1 hold rows p = HP w .. HP w + HP - 1, slots
+// HP..2HP-1 their mirrors 128 - p; pair p = 0 is {0, 64} (both
+// self-mirrored).
+template <int RPW>
 __device__ __forceinline__ int fwd_row(int w, int rho) {
-    const int p = 8 * w + (rho & 7);
-    return rho < 8 ? p : (p == 0 ? 64 : 128 - p);
+    constexpr int HP = RPW / 2;
+    const int p = HP * w + (rho & (HP - 1));
+    return rho < HP ? p : (p == 0 ? 64 : 128 - p);
 }
 
-// Row FFTs of one 16-row tile, results left in LDS as Z_row[k2] at
-// lds[rho*US + pad16(k2)] (a barrier follows).
+// Row FFTs of one tile of 256-column rows (16 threads per row), results
+// left in LDS as Z_row[k2] at lds[rho*US + pad16(k2)] (a barrier follows).
 // vhold / shold: a per-thread value and 16 workgroup-uniform values loaded
 // before the call that must arrive with the row data (the untangle
 // twiddles), so their loads are not deferred past the barriers.
 template <bool HOLD>
 __device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, float2* lds, float2* tw2,
-                                               int rho, int t, const float2* __restrict__ tws, float2* vhold,
-                                               float2* shold) {
+                                               int rho, int t, int nthreads, const float2* __restrict__ tws,
+                                               float2* vhold, float2* shold) {
     using P = Plan<256>;
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = yrow[t + 16 * r];
-    load_tw2_lds<256>(tw2, tws, threadIdx.x, 256);
+    load_tw2_lds<256>(tw2, tws, threadIdx.x, nthreads);
     if constexpr (HOLD) {
         asm volatile("" : "+v"(vhold->x), "+v"(vhold->y));
 #pragma unroll
@@ -287,33 +326,36 @@ __device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, 
     __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, float2* __restrict__ xs,
-                                                 const float2* __restrict__ twn,
-                                                 const float2* __restrict__ tws) {
+template <int RPW>
+__global__ __launch_bounds__(16 * RPW) void k_row_fwd(const float2* __restrict__ in, float2* __restrict__ xs,
+                                                      const float2* __restrict__ twn,
+                                                      const float2* __restrict__ tws) {
     using P = Plan<256>;
-    __shared__ float2 lds[kRowsPerWg * P::US];
+    constexpr int kWgs = 128 / RPW;               // workgroups per slice
+    __shared__ float2 lds[RPW * P::US];
     __shared__ float2 tw2[tw2_len<256>()];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int b = lg / kRowWgs;
-    const int w = lg - b * kRowWgs;
+    const int b = lg / kWgs;
+    const int w = lg - b * kWgs;
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
     // untangle twiddles of this thread's output bins, loaded up front:
     // W_N^{k1 + 128 (kg + 16 u)} = W_N^{k1 + 128 kg} W_N^{2048 u}, the second
     // factor the same for the whole workgroup (one rounding more than a table value)
-    const int rho2 = threadIdx.x & 15;
-    const int kg = threadIdx.x >> 4;
-    const int k1 = fwd_row(w, rho2);
+    const int rho2 = threadIdx.x & (RPW - 1);     // output lanes walk the tile's rows
+    const int kg = threadIdx.x / RPW;             // < 16
+    const int k1 = fwd_row<RPW>(w, rho2);
     float2 wb = twn[k1 + 128 * kg];
     float2 wu[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) wu[u] = twn[2048 * u];
-    row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row(w, rho) * 256, lds, tw2, rho, t, tws, &wb, wu);
+    row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row<RPW>(w, rho) * 256, lds, tw2, rho, t, 16 * RPW, tws,
+                         &wb, wu);
     // untangle: lanes walk the tile's rows for coalesced stores
     const float2* s = lds + rho2 * P::US;
     // mirror bin L - k: row 128 - k1 at column 255 - k2; rows 0 and 64 are
     // their own mirrors (row 0 at column (256 - k2) mod 256)
-    const float2* mp = (k1 == 0 || k1 == 64) ? s : lds + (rho2 ^ 8) * P::US;
+    const float2* mp = (k1 == 0 || k1 == 64) ? s : lds + (rho2 ^ (RPW / 2)) * P::US;
     const int mcol = k1 == 0 ? 256 : 255;
     float2* xb = xs + (long)b * kXStride;
 #pragma unroll
@@ -334,22 +376,24 @@ __global__ __launch_bounds__(256) void k_row_fwd(const float2* __restrict__ in, 
     }
 }
 
-__global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, float2* __restrict__ y,
-                                                 const float2* __restrict__ tws) {
+template <int RPW>
+__global__ __launch_bounds__(16 * RPW) void k_row_inv(const float2* __restrict__ in, float2* __restrict__ y,
+                                                      const float2* __restrict__ tws) {
     using P = Plan<256>;
-    __shared__ float2 lds[kRowsPerWg * P::US];
+    constexpr int kWgs = 128 / RPW;               // workgroups per slice
+    __shared__ float2 lds[RPW * P::US];
     __shared__ float2 tw2[tw2_len<256>()];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int b = lg / kRowWgs;
-    const int rg = lg - b * kRowWgs;
+    const int b = lg / kWgs;
+    const int rg = lg - b * kWgs;
     const int rho = threadIdx.x >> 4;
     const int t = threadIdx.x & 15;
-    row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * kRowsPerWg + rho) * 256, lds, tw2, rho, t, tws,
+    row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * RPW + rho) * 256, lds, tw2, rho, t, 16 * RPW, tws,
                           nullptr, nullptr);
-    const int rho2 = threadIdx.x & 15;
-    const int kg = threadIdx.x >> 4;
+    const int rho2 = threadIdx.x & (RPW - 1);
+    const int kg = threadIdx.x / RPW;
     const float2* s2 = lds + rho2 * P::US;
-    const int kk1 = rg * kRowsPerWg + rho2;
+    const int kk1 = rg * RPW + rho2;
     constexpr float sc = 0.5f / (float)kL;     // 1/L of the inverse, 1/2 of the retangle
     float2* yo = y + (long)b * kL;  // y viewed as [batch][32768] float pairs
 #pragma unroll
@@ -358,6 +402,47 @@ __global__ __launch_bounds__(256) void k_row_inv(const float2* __restrict__ in, 
         const float2 w = s2[pad16(k2)];
         yo[kk1 + 128 * k2] = make_float2(w.x * sc, -w.y * sc);
     }
+}
+
+// Launch helpers: the pass kernels of one direction in the tile shape the
+// batch size selects.
+template <int CPW, int RPW>
+static int launch_fwd_passes(const float2* x, float2* work, float2* xs, const float2* twp, const float2* twh,
+                             const float2* tws, const SliceSrc& src, bool sliced, int64_t batch,
+                             hipStream_t stream) {
+    const dim3 gc((unsigned)(batch * (256 / CPW))), gr((unsigned)(batch * (128 / RPW)));
+    if (sliced)
+        hipLaunchKernelGGL((k_col_fwd<true, CPW>), gc, dim3(8 * CPW), 0, stream, x, work, twp, tws, src);
+    else
+        hipLaunchKernelGGL((k_col_fwd<false, CPW>), gc, dim3(8 * CPW), 0, stream, x, work, twp, tws, src);
+    if (int e = launch_status()) return e;
+    hipLaunchKernelGGL((k_row_fwd<RPW>), gr, dim3(16 * RPW), 0, stream, work, xs, twh, tws);
+    return launch_status();
+}
+
+static int fwd_passes(const float2* x, float2* work, float2* xs, const float2* twp, const float2* twh,
+                      const float2* tws, const SliceSrc& src, bool sliced, int64_t batch, hipStream_t stream) {
+    if (batch <= kNarrowMaxBatch)
+        return launch_fwd_passes<kColsNarrow, kRowsNarrow>(x, work, xs, twp, twh, tws, src, sliced, batch, stream);
+    return launch_fwd_passes<kColsWide, kRowsWide>(x, work, xs, twp, twh, tws, src, sliced, batch, stream);
+}
+
+template <int CPW, int RPW>
+static int launch_inv_passes(const float2* f, float2* work, float2* y, const float2* twp, const float2* twh,
+                             const int* ovf, const float2* tws, int64_t batch, hipStream_t stream) {
+    hipLaunchKernelGGL((k_col_inv<CPW>), dim3((unsigned)(batch * (256 / CPW))), dim3(8 * CPW), 0, stream, f, work,
+                       twp, twh, ovf, tws);
+    if (int e = launch_status()) return e;
+    hipLaunchKernelGGL((k_row_inv<RPW>), dim3((unsigned)(batch * (128 / RPW))), dim3(16 * RPW), 0, stream, work,
+                       y, tws);
+    return launch_status();
+}
+
+static int inv_passes(const float2* f, float2* work, float2* y, const float2* twp, const float2* twh, const int* ovf,
+                      const float2* tws, int64_t batch, hipStream_t stream) {
+    if (batch <= kNarrowMaxBatch)
+        return launch_inv_passes<kInvColsNarrow, kRowsNarrow>(f, work, y, twp, twh, ovf, tws, batch, stream);
+    return launch_inv_passes<kInvColsWide, kRowsWide>(f, work, y, twp, twh, ovf, tws, batch, stream);
 }
 
 }  // namespace fcqt
@@ -371,15 +456,10 @@ extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float
     if (!aligned(x, 8) || !aligned(xs, 8) || !aligned(work, 8) || !aligned(tab->tw_pass, 8) ||
         !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
         return FCQT_EALIGN;
-    const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
-    hipLaunchKernelGGL(k_col_fwd<false>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
-                       reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
-                       reinterpret_cast<const float2*>(tab->tw_pass), tws, SliceSrc{nullptr, nullptr, 1, 1, 0, 0});
-    if (int e = launch_status()) return e;
-    hipLaunchKernelGGL(k_row_fwd, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
-                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(xs),
-                       reinterpret_cast<const float2*>(tab->tw_half), tws);
-    return launch_status();
+    return fwd_passes(reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
+                      reinterpret_cast<float2*>(xs), reinterpret_cast<const float2*>(tab->tw_pass),
+                      reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const float2*>(tab->tw_stage),
+                      SliceSrc{nullptr, nullptr, 1, 1, 0, 0}, false, batch, stream);
 }
 
 extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float* f, float* y,
@@ -389,15 +469,10 @@ extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, c
     if (!aligned(f, 16) || !aligned(y, 8) || !aligned(work, 8) || !aligned(tab->tw_pass, 8) ||
         !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16) || !aligned(ovf, 4))
         return FCQT_EALIGN;
-    const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
-    hipLaunchKernelGGL(k_col_inv, dim3((unsigned)(batch * kInvWgs)), dim3(kInvThreads), 0, stream,
-                       reinterpret_cast<const float2*>(f), reinterpret_cast<float2*>(work),
-                       reinterpret_cast<const float2*>(tab->tw_pass),
-                       reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const int*>(ovf), tws);
-    if (int e = launch_status()) return e;
-    hipLaunchKernelGGL(k_row_inv, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
-                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(y), tws);
-    return launch_status();
+    return inv_passes(reinterpret_cast<const float2*>(f), reinterpret_cast<float2*>(work),
+                      reinterpret_cast<float2*>(y), reinterpret_cast<const float2*>(tab->tw_pass),
+                      reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const int*>(ovf),
+                      reinterpret_cast<const float2*>(tab->tw_stage), batch, stream);
 }
 
 extern "C" int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int64_t sig_len, const float* window,
@@ -412,15 +487,11 @@ extern "C" int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int6
         !aligned(tab->tw_pass, 8) || !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
         return FCQT_EALIGN;
     const int64_t batch = nsig * nslices;
-    const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
-    hipLaunchKernelGGL(k_col_fwd<true>, dim3((unsigned)(batch * kColWgs)), dim3(128), 0, stream,
-                       nullptr, reinterpret_cast<float2*>(work), reinterpret_cast<const float2*>(tab->tw_pass), tws,
-                       SliceSrc{sig, window, (long)sig_len, (int)nslices, (long)first, (long)origin});
-    if (int e = launch_status()) return e;
-    hipLaunchKernelGGL(k_row_fwd, dim3((unsigned)(batch * kRowWgs)), dim3(256), 0, stream,
-                       reinterpret_cast<const float2*>(work), reinterpret_cast<float2*>(xs),
-                       reinterpret_cast<const float2*>(tab->tw_half), tws);
-    return launch_status();
+    return fwd_passes(nullptr, reinterpret_cast<float2*>(work), reinterpret_cast<float2*>(xs),
+                      reinterpret_cast<const float2*>(tab->tw_pass), reinterpret_cast<const float2*>(tab->tw_half),
+                      reinterpret_cast<const float2*>(tab->tw_stage),
+                      SliceSrc{sig, window, (long)sig_len, (int)nslices, (long)first, (long)origin}, true, batch,
+                      stream);
 }
 
 namespace fcqt {

@@ -129,19 +129,33 @@ def _c(t):
     return t[:, 0].astype(np.complex128) + 1j * t[:, 1].astype(np.complex128)
 
 
-def col_fwd(x):
-    """k_col_fwd: x [B, N] real -> Y [B, L] (rows k1, columns n2)."""
+# Tile shapes of the pass kernels (packed_fft.hip): wide (the default) and
+# the narrow shapes that batches up to NARROW_MAX_BATCH run.
+WIDE = dict(cols=16, rows=16, inv_cols=32)
+NARROW = dict(cols=8, rows=8, inv_cols=16)
+NARROW_MAX_BATCH = 16
+FOLD_LISTS = 256 // WIDE["inv_cols"]
+
+
+def col_fwd(x, cpw=16):
+    """k_col_fwd with CPW columns per workgroup: x [B, N] real -> Y [B, L]
+    (rows k1, columns n2); every element of Y written exactly once."""
     x = np.asarray(x, dtype=np.float64)
     B = x.shape[0]
     z = x[:, 0::2] + 1j * x[:, 1::2]
     twp = _c(T.pass_twiddles())
     Y = np.empty((B, L), dtype=np.complex128)
-    c = np.arange(16)
+    hits = np.zeros(L, dtype=np.int64)
+    tid = np.arange(8 * cpw)
+    c_of, t_of = tid & (cpw - 1), tid // cpw
+    assert t_of.max() < 8
+    c = np.arange(cpw)
     tt = np.arange(8)
     for b in range(B):
-        for cg in range(16):
-            n2 = cg * 16 + c
-            v = np.empty((16, 8, 16), dtype=np.complex128)    # [unit=c, t, r]
+        for cg in range(256 // cpw):
+            n2 = cg * cpw + c
+            assert np.array_equal(np.sort(cg * cpw + c_of), np.repeat(n2, 8))
+            v = np.empty((cpw, 8, 16), dtype=np.complex128)    # [unit=c, t, r]
             for r in range(16):
                 idx = 256 * (tt[None, :] + 8 * r) + n2[:, None]
                 assert idx.max() < L
@@ -153,33 +167,43 @@ def col_fwd(x):
                     o = k1[None, :] * 256 + n2[:, None]
                     assert o.max() < L
                     Y[b][o] = v[:, :, q * 8 + r] * twp[o]
+                    if b == 0:
+                        np.add.at(hits, o.ravel(), 1)
+    assert np.all(hits == 1)
     return Y
 
 
-def fwd_row(w, rho):
-    p = 8 * w + (rho & 7)
-    return p if rho < 8 else (64 if p == 0 else 128 - p)
+def fwd_row(w, rho, rpw=16):
+    hp = rpw // 2
+    p = hp * w + (rho & (hp - 1))
+    return p if rho < hp else (64 if p == 0 else 128 - p)
 
 
-def row_fwd(Y):
-    """k_row_fwd: paired row FFTs + untangle -> X [B, L+1] (rfft)."""
+def row_fwd(Y, rpw=16):
+    """k_row_fwd with RPW rows per workgroup: paired row FFTs + untangle ->
+    X [B, L+1] (rfft); each bin written exactly once, by the lane mapping
+    of the kernel's store loop."""
     B = Y.shape[0]
     twn = _c(T.half_twiddles())
     X = np.full((B, L + 1), np.nan + 0j)
+    hits = np.zeros(L + 1, dtype=np.int64)
     t = np.arange(16)
+    tid = np.arange(16 * rpw)
+    rho2_of, kg_of = tid & (rpw - 1), tid // rpw
+    assert kg_of.max() < 16
     for b in range(B):
-        for w in range(8):
-            rows = np.array([fwd_row(w, rho) for rho in range(16)])
-            v = np.empty((16, 16, 16), dtype=np.complex128)
+        for w in range(128 // rpw):
+            rows = np.array([fwd_row(w, rho, rpw) for rho in range(rpw)])
+            v = np.empty((rpw, 16, 16), dtype=np.complex128)
             for r in range(16):
                 v[:, :, r] = Y[b][rows[:, None] * 256 + (t[None, :] + 16 * r)]
             v = fft_unit(v, 256, -1)
-            Zr = np.empty((16, 256), dtype=np.complex128)       # LDS: row rho, column k2
+            Zr = np.empty((rpw, 256), dtype=np.complex128)       # LDS: row rho, column k2
             for r in range(16):
                 Zr[:, t + 16 * r] = v[:, :, r]
-            for rho2 in range(16):
+            for rho2, kg in zip(rho2_of, kg_of):
                 k1 = rows[rho2]
-                k2 = np.arange(256)
+                k2 = kg + 16 * np.arange(16)
                 k = k1 + 128 * k2
                 z = Zr[rho2, k2]
                 if k1 == 0:
@@ -187,41 +211,57 @@ def row_fwd(Y):
                 elif k1 == 64:
                     zm = Zr[rho2, 255 - k2]
                 else:
-                    assert rows[rho2 ^ 8] == 128 - k1
-                    zm = Zr[rho2 ^ 8, 255 - k2]
+                    assert rows[rho2 ^ (rpw // 2)] == 128 - k1
+                    zm = Zr[rho2 ^ (rpw // 2), 255 - k2]
                 wn = twn[k]
                 ca = 0.5 * (1 + wn.imag) - 0.5j * wn.real
                 cb = 0.5 * (1 - wn.imag) + 0.5j * wn.real
                 X[b][k] = ca * z + cb * np.conj(zm)
+                if b == 0:
+                    np.add.at(hits, k, 1)
             if w == 0:
+                assert rows[0] == 0
                 z0 = Zr[0, 0]
                 X[b][L] = z0.real - z0.imag
+                if b == 0:
+                    hits[L] += 1
+    assert np.all(hits == 1)
     assert not np.isnan(X).any()
     return X
 
 
-def packed_fft_fwd(x):
+def packed_fft_fwd(x, shape=WIDE):
     """Forward passes of packed_fft.hip: x [B, N] -> X = rfft(x) [B, L+1]."""
-    return row_fwd(col_fwd(x))
+    return row_fwd(col_fwd(x, shape["cols"]), shape["rows"])
 
 
-def _row_pass(Y, inverse):
+def _row_pass(Y, inverse, rpw=16):
+    """k_row_inv with RPW rows per workgroup: row FFTs, stored through the
+    kernel's lane mapping at k1 + 128 k2 (each element exactly once)."""
     B = Y.shape[0]
     out = np.empty((B, L), dtype=np.complex128)
+    hits = np.zeros(L, dtype=np.int64)
     t = np.arange(16)
+    tid = np.arange(16 * rpw)
+    rho2_of, kg_of = tid & (rpw - 1), tid // rpw
     for b in range(B):
-        for rg in range(8):
-            k1 = rg * 16 + np.arange(16)
-            v = np.empty((16, 16, 16), dtype=np.complex128)
+        for rg in range(128 // rpw):
+            k1 = rg * rpw + np.arange(rpw)
+            v = np.empty((rpw, 16, 16), dtype=np.complex128)
             for r in range(16):
                 v[:, :, r] = Y[b][(k1[:, None] * 256) + (t[None, :] + 16 * r)]
             v = fft_unit(v, 256, -1)
-            # transpose through LDS then store at k1 + 128 k2
+            Zr = np.empty((rpw, 256), dtype=np.complex128)
+            for r in range(16):
+                Zr[:, t + 16 * r] = v[:, :, r]
             for u in range(16):
-                k2 = np.arange(16) + 16 * u      # kg = 0..15
-                o = k1[:, None] + 128 * k2[None, :]
+                k2 = kg_of + 16 * u
+                o = rg * rpw + rho2_of + 128 * k2
                 assert o.max() < L
-                out[b][o] = v[:, k2 % 16, k2 // 16]
+                out[b][o] = Zr[rho2_of, k2]
+                if b == 0:
+                    np.add.at(hits, o, 1)
+    assert np.all(hits == 1)
     if inverse:
         return out / L
     return out
@@ -247,58 +287,125 @@ def staged_bins(Fs, fold):
     return out
 
 
-def inv_col(w, c):
-    p = 16 * w + (c & 15)
-    return p if c < 16 else (128 if p == 0 else 256 - p)
+def inv_col(w, c, cpw=32):
+    h = cpw // 2
+    p = h * w + (c & (h - 1))
+    return p if c < h else (128 if p == 0 else 256 - p)
 
 
-def packed_fft_inv(F, ovf=None):
+US128 = Plan(128).US
+
+
+def col_inv_stage(Fs, fold, w, cpw=32):
+    """LDS of inverse column workgroup w (CPW columns) after its staging
+    phase, by the kernel's own arithmetic: slot c holds column
+    inv_col(w, c) at [c US + n1] (plane sum), bin L at [128] of slot 0 in
+    workgroup 0, and each fold-list entry of the containing wide list is
+    added at the position the kernel computes, if this workgroup owns it.
+    Returns (lds, entries used)."""
+    h = cpw // 2
+    nthreads = 8 * cpw
+    share = (256 // cpw) // FOLD_LISTS
+    nent = T.FOLD_PER_WG // nthreads
+    assert share * FOLD_LISTS == 256 // cpw and nent * nthreads == T.FOLD_PER_WG
+    lds = np.full(cpw * US128, np.nan + 0j)
+    n1 = np.arange(128)
+    for c in range(cpw):
+        col = inv_col(w, c, cpw)
+        lds[c * US128 + n1] = Fs[256 * n1 + col] + Fs[T.FSTRIDE + 256 * n1 + col]
+        if col == 0:
+            assert c == 0 and w == 0
+            lds[128] = Fs[L] + Fs[T.FSTRIDE + L]
+    used = []
+    lst = fold[(w // share) * T.FOLD_PER_WG:(w // share + 1) * T.FOLD_PER_WG]
+    for tid in range(nthreads):
+        for e in range(nent):
+            ent = int(lst[tid + e * nthreads])
+            if ent < 0:
+                continue
+            b = ent & 0xFFFF
+            pos = -1
+            if b >= L:
+                if w == 0:
+                    pos = 128
+            else:
+                cl, r1 = b & 255, b >> 8
+                pp = (0 if cl == 128 else cl) if cl <= 128 else 256 - cl
+                if pp // h == w:
+                    pos = ((0 if cl < 128 else h) + (pp & (h - 1))) * US128 + r1
+                    assert inv_col(w, pos // US128, cpw) == cl and pos % US128 == r1
+            if pos >= 0:
+                assert 0 <= pos < cpw * US128
+                k = min(ent >> 16, T.OVF_CAP - 1)
+                o = 2 * T.FSTRIDE + 2 * k
+                lds[pos] += Fs[o] + Fs[o + 1]
+                used.append(ent)
+    return lds, used
+
+
+def packed_fft_inv(F, ovf=None, shape=WIDE):
     """k_col_inv (paired columns, retangle from staged bins) + k_row_inv.
     F is a plain half spectrum [B, L+1] or, with the fold lists, the slot
-    buffer [B, FROW]."""
+    buffer [B, FROW] (then staged through col_inv_stage, and every fold
+    entry must be consumed exactly once)."""
+    cpw, rpw = shape["inv_cols"], shape["rows"]
+    h = cpw // 2
     F = np.asarray(F, dtype=np.complex128)
     B = F.shape[0]
     twn = _c(T.half_twiddles())
     twp = _c(T.pass_twiddles())
     Y = np.empty((B, L), dtype=np.complex128)
+    hits = np.zeros(L, dtype=np.int64)
     tt = np.arange(8)
     n1s = np.arange(128)
     for b in range(B):
-        Fb = F[b] if ovf is None else staged_bins(F[b], ovf)
-        get = lambda i: Fb[i]
-        nyq = get(np.array([L]))[0]
-        for w in range(T.INV_WGS):
-            cols = np.array([inv_col(w, c) for c in range(T.INV_COLS_PER_WG)])
-            raw = get(256 * n1s[None, :] + cols[:, None])       # staged [c][n1]
-            v = np.empty((T.INV_COLS_PER_WG, 8, 16), dtype=np.complex128)
+        used = []
+        if ovf is None:
+            plain = np.zeros(T.FROW, dtype=np.complex128)
+            plain[:L + 1] = F[b]
+        for w in range(256 // cpw):
+            cols = np.array([inv_col(w, c, cpw) for c in range(cpw)])
+            if ovf is None:
+                lds, _ = col_inv_stage(plain, np.full(T.INV_WGS * T.FOLD_PER_WG, -1), w, cpw)
+            else:
+                lds, u = col_inv_stage(F[b], ovf, w, cpw)
+                used += u
+            raw = lds.reshape(cpw, US128)
+            if w == 0:
+                raw[0, 0] = raw[0, 0].real      # bins 0 and L are real for irfft
+                raw[0, 128] = raw[0, 128].real
+            v = np.empty((cpw, 8, 16), dtype=np.complex128)
             for r in range(16):
                 n1 = tt + 8 * r
-                for c in range(T.INV_COLS_PER_WG):
+                for c in range(cpw):
                     col = cols[c]
                     i = 256 * n1 + col
                     f0 = raw[c, n1].copy()
                     if col == 0:
-                        f1 = np.where(n1 == 0, nyq, raw[c, (128 - n1) % 128])
+                        f1 = raw[c, 128 - n1]
                     elif col == 128:
                         f1 = raw[c, 127 - n1]
                     else:
-                        assert cols[c ^ 16] == 256 - col
-                        f1 = raw[c ^ 16, 127 - n1]
-                    f1 = f1.copy()
-                    zero = i == 0
-                    f0[zero] = f0[zero].real
-                    f1[zero] = f1[zero].real
+                        assert cols[c ^ h] == 256 - col
+                        f1 = raw[c ^ h, 127 - n1]
                     e = 0.5 * (f0 + np.conj(f1))
                     d = 0.5 * (f0 - np.conj(f1))
                     o = d * np.conj(twn[i])
                     v[c, :, r] = np.conj(e + 1j * o)
+            assert not np.isnan(v).any()
             v = fft_unit(v, 128, -1)
             for q in range(2):
                 for r in range(8):
                     k1 = tt + 8 * q + 16 * r
                     o = k1[None, :] * 256 + cols[:, None]
                     Y[b][o] = v[:, :, q * 8 + r] * twp[o]
-    zp = _row_pass(Y, inverse=True)
+                    if b == 0:
+                        np.add.at(hits, o.ravel(), 1)
+        if ovf is not None:
+            listed = [e for e in np.asarray(ovf).tolist() if e >= 0]
+            assert sorted(used) == sorted(listed)
+    assert np.all(hits == 1)
+    zp = _row_pass(Y, inverse=True, rpw=rpw)
     y = np.empty((B, N))
     y[:, 0::2] = zp.real
     y[:, 1::2] = -zp.imag

@@ -137,13 +137,16 @@ def test_analysis_layouts_agree_bitwise(fused):
 
 
 def test_analysis_batch_independent_bitwise(fused):
+    """Rows of a B = 16 and a B = 64 analysis (narrow and wide pass tiles)
+    equal their batch-1 results bit for bit."""
     rs = np.random.RandomState(7)
-    x = rs.standard_normal((16, N)).astype(np.float32)
-    KR, KI = fused.fwd(gpu(x))
-    full = torch.complex(KR, KI).clone()
-    for b in (0, 5, 15):
-        kr1, ki1 = fused.fwd(gpu(x[b:b + 1]))
-        assert torch.equal(torch.complex(kr1, ki1)[0], full[b])
+    x = rs.standard_normal((64, N)).astype(np.float32)
+    for B in (16, 64):
+        KR, KI = fused.fwd(gpu(x[:B]))
+        full = torch.complex(KR, KI).clone()
+        for b in (0, 5, B - 1):
+            kr1, ki1 = fused.fwd(gpu(x[b:b + 1]))
+            assert torch.equal(torch.complex(kr1, ki1)[0], full[b])
 
 
 # ----------------------------------------------------------- synthesis
@@ -267,12 +270,16 @@ def test_linearity_full_batch(fused):
 
 
 def test_synthesis_batch_independent_bitwise(fused):
+    """Rows of a B = 64 synthesis (wide pass tiles) equal their batch-1
+    and batch-4 results (narrow tiles) bit for bit."""
     rs = np.random.RandomState(1616)
-    C = (rs.standard_normal((16, fused.ncoef)) + 1j * rs.standard_normal((16, fused.ncoef))).astype(np.complex64)
+    C = (rs.standard_normal((64, fused.ncoef)) + 1j * rs.standard_normal((64, fused.ncoef))).astype(np.complex64)
     y = fused.bwd(gpu(C.real), gpu(C.imag)).clone()
-    for b in (0, 7, 15):
+    for b in (0, 31, 63):
         y1 = fused.bwd(gpu(C.real[b:b + 1]), gpu(C.imag[b:b + 1]))
         assert torch.equal(y1[0], y[b])
+    y4 = fused.bwd(gpu(C.real[8:12]), gpu(C.imag[8:12]))
+    assert torch.equal(y4, y[8:12])
 
 
 def test_side_bands_dropped_like_oracle(train, oracle):

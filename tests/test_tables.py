@@ -6,6 +6,8 @@ factored tables, replayed through the kernels' exact schedule
 (tests/kernel_sim.py), must reproduce the oracle's analysis, synthesis and
 both adjoints (the analogue of the reference's CPU table gates,
 bench/radix_gpu.py:51-120 and bench/autograd_check.py)."""
+import pathlib
+
 import numpy as np
 import pytest
 import torch
@@ -16,6 +18,7 @@ from oracle.cqt_oracle import snr_db
 from test_oracle import group_hashes
 
 N = 65536
+ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 
 def test_package_tables_bit_exact(pkg_cqt_cpu, golden):
@@ -305,3 +308,38 @@ def test_graphed_input_check_cpu():
         _check_inputs(rec, list(_leaves((torch.ones(1, 8), [torch.ones(3)]))))
     with pytest.raises(ValueError, match="input tensors"):
         _check_inputs(rec, list(_leaves((torch.ones(4, 8),))))
+
+
+def test_narrow_pass_shapes_equal_wide_cpu(factored_tables):
+    """The narrow tile shapes of the pass kernels (batches up to
+    ks.NARROW_MAX_BATCH) replayed with their own index arithmetic: every
+    output element written once, every fold-list entry consumed once by the
+    narrow workgroup that owns its column, LDS positions in bounds, and the
+    results equal the wide shapes' exactly (same per-column arithmetic)."""
+    t = factored_tables
+    rs = np.random.RandomState(21)
+    x = rs.standard_normal((1, N))
+    Xw = ks.packed_fft_fwd(x, ks.WIDE)
+    Xn = ks.packed_fft_fwd(x, ks.NARROW)
+    assert np.array_equal(Xw, Xn)
+    assert snr_db(np.fft.rfft(x), Xn) > 140
+    for table in ("scat", "scat_a"):
+        G = rs.standard_normal((1, t["ncoef"])) + 1j * rs.standard_normal((1, t["ncoef"]))
+        F = ks.scatter_bands(G, t[table + "_taps"], t["tasks"], t["ncoef"])
+        yw = ks.packed_fft_inv(F, t["ovf_" + table], ks.WIDE)
+        yn = ks.packed_fft_inv(F, t["ovf_" + table], ks.NARROW)
+        assert np.array_equal(yw, yn)
+        ref = np.fft.irfft(ks.staged_bins(F[0], t["ovf_" + table])[None, :], n=N)
+        assert snr_db(ref, yn) > 140
+
+
+def test_narrow_shape_constants_match_kernels_cpu():
+    """The simulator's tile shapes and batch threshold are the kernels'."""
+    src = (ROOT / "flash-cqt_amd" / "csrc" / "packed_fft.hip").read_text()
+    import re
+    def const(name):
+        return int(re.search(rf"\b{name}\s*=\s*(\d+)", src).group(1))
+    assert const("kColsWide") == ks.WIDE["cols"] and const("kColsNarrow") == ks.NARROW["cols"]
+    assert const("kRowsWide") == ks.WIDE["rows"] and const("kRowsNarrow") == ks.NARROW["rows"]
+    assert const("kInvColsWide") == ks.WIDE["inv_cols"] and const("kInvColsNarrow") == ks.NARROW["inv_cols"]
+    assert const("kNarrowMaxBatch") == ks.NARROW_MAX_BATCH
