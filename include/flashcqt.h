@@ -19,7 +19,10 @@
  *   - Return value: FCQT_OK (0), or an FCQT_E* code. Argument errors are
  *     detected before any HIP call is made.
  *   - Calls that share a workspace must be ordered on one stream.
- *   - Results are deterministic: no kernel uses atomics.
+ *   - Results are deterministic: no kernel uses atomics. They are also
+ *     independent of the batch size: a slice gives the same bits alone or
+ *     in any batch (the launchers pick the FFT passes' tile shape by batch
+ *     size; every shape does the same arithmetic per slice).
  *
  * Fixed geometry (the reference's fused path hard-requires it,
  * fused.py:230): N = 65536 real samples per slice, L = N/2 = 32768.
