@@ -511,12 +511,13 @@ def test_sliced_fused_framing_equals_engine_composition():
     assert torch.equal(y3, y4.detach())
 
 
-@pytest.mark.parametrize("length", [1, 1000, 16384, 32768, 32769, 65536, 131071])
+@pytest.mark.parametrize("length", [1, 1000, 16384, 32768, 32769, 65536, 131071, 262144])
 def test_sliced_fused_ragged_lengths(length):
     """Short, hop-aligned and ragged signal lengths, two channels: the fused
     framing equals the host framing around the same engine bit for bit
     (forward blocks, trimmed and untrimmed inverse), and the round trip
-    holds its SNR."""
+    holds its SNR. 262144 samples is the reference's own sliced round-trip
+    gate (bench/sliced.py:92-101, > 120 dB there)."""
     from flash_cqt import SlicedCQT
     s = SlicedCQT(device=_dev())
     rs = np.random.RandomState(length)
