@@ -18,8 +18,9 @@ configs[2]); batch 1 (configs[1], sinusoids + noise) and batch 16 are in
   - the SlicedCQT streaming workload (configs[4]) in "sliced";
   - the TrainableCQT differentiable step in "training_step".
 Per-kernel launch durations are timed with hipEvents on the launch stream
-(graphs of back-to-back launches); "roofline" reports the dominant kernel's
-algorithmic bytes per launch over its duration against 8 TB/s.
+around back-to-back stream launches (graphs of the same launches beside
+them); "roofline" reports the dominant kernel's algorithmic bytes per launch
+over its duration against 8 TB/s.
 
 Extra modes (for rocprofv3 counter runs): --kernels-only runs a few
 launches of every kernel plus a plain copy of known size (the calibration
