@@ -536,6 +536,10 @@ def main():
     gbps = B * SLICE_RT_BYTES / (ms_step * 1e-3) / 1e9
 
     kern = kernel_timings(f, B, args.kernel_reps)
+    # per-kernel rates at the other batch of configs[2] (16) too
+    for b in (16,):
+        if b in per_batch and b != B:
+            per_batch[b]["kernels"] = kernel_timings(f, b, args.kernel_reps)
     single = {k: v for k, v in kern.items() if v["launches"] == 1}
     dom = max(single, key=lambda k: single[k]["ms_per_launch"])
     ach = kern[dom]["gbps"]
