@@ -129,6 +129,8 @@ class SlicedCQT:
         key = (L, S, first & 1, c0, str(device))
         cache = self.__dict__.setdefault("_frame_cache", {})
         if key not in cache:
+            if len(cache) >= 8:                 # a few signal lengths at a time (24 B per map entry)
+                cache.pop(next(iter(cache)))
             g = torch.arange(first & 1, (first & 1) + S, device=device).view(-1, 1)
             j = torch.arange(N, device=device).view(1, -1)
             jj = (j + torch.where(g % 2 == 0, H, N - H)) % N
