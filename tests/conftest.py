@@ -19,6 +19,18 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (run with -m gpu)")
 
 
+def pytest_sessionstart(session):
+    """Build the HIP library once if this checkout has none yet (a fresh
+    clone); a built library is used as it is."""
+    lib = ROOT / "flash-cqt_amd" / "flash_cqt" / "_lib" / "libflashcqt.so"
+    if not lib.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("flashcqt_build", ROOT / "flash-cqt_amd" / "build.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build(verbose=False)
+
+
 @pytest.fixture(scope="session")
 def golden():
     return np.load(GOLDEN, allow_pickle=False)
