@@ -187,8 +187,14 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
     }
 }
 
+// REVERSE: walk each XCD's range from its end (the scatter follows the
+// route kernel on the same (task, slice) grid, so it starts with the
+// coefficients the route kernel wrote last; measured 0.2-0.9 us per round
+// trip at B = 16-120, same results).
+template <bool REVERSE>
 __device__ __forceinline__ void decode_task(int batch, int& task, int& b) {
-    const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int lg = REVERSE ? xcd_remap_reverse((int)blockIdx.x, (int)gridDim.x)
+                           : xcd_remap((int)blockIdx.x, (int)gridDim.x);
     task = lg / batch;
     b = lg - task * batch;
 }
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
     __shared__ float2 lds[kBandLds];
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
-    decode_task(batch, task_id, b);
+    decode_task<false>(batch, task_id, b);
     // the records issue first (they need the task index only); the task
     // record then selects the band length, and the gathers follow inside
     int2 rv[16];
@@ -236,7 +242,7 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
     __shared__ float2 lds[kBandLds];
     __shared__ float2 tw2[tw2_len<2048>()];
     int task_id, b;
-    decode_task(batch, task_id, b);
+    decode_task<true>(batch, task_id, b);
     const int4 td = tasks[task_id];
 #define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT>(td, task_id, b, batch, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
     switch (td.x) {

@@ -381,4 +381,15 @@ __device__ __forceinline__ int xcd_remap(int lin, int G) {
     return xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
 }
 
+// The same per-XCD ranges walked from their ends: a kernel that reads what
+// the previous kernel of the same grid wrote starts with that kernel's
+// last (most recently written, still cached) workgroups. Bijective on [0, G).
+__device__ __forceinline__ int xcd_remap_reverse(int lin, int G) {
+    const int q = G >> 3, rem = G & 7;
+    const int xcd = lin & 7, idx = lin >> 3;
+    const int n = xcd < rem ? q + 1 : q;
+    const int start = xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q;
+    return start + (n - 1 - idx);
+}
+
 }  // namespace fcqt

@@ -520,3 +520,22 @@ def stream_overlap(y, tail, k):
     a = y[:, (p + sh) & (N - 1)]
     b = y[:, (p + 2 * H + sh) & (N - 1)]
     return (tail + a if k > 0 else None), b
+
+
+# ------------------------------------------------------------ XCD mapping
+
+def xcd_remap(lin, G):
+    """fcqt_fft.hpp xcd_remap: dispatch id -> logical id, each of the 8 XCDs
+    (ids lin & 7) receiving one contiguous range."""
+    q, rem = G >> 3, G & 7
+    x, i = lin & 7, lin >> 3
+    return x * (q + 1) + i if x < rem else rem * (q + 1) + (x - rem) * q + i
+
+
+def xcd_remap_reverse(lin, G):
+    """fcqt_fft.hpp xcd_remap_reverse: the same ranges, walked from the end."""
+    q, rem = G >> 3, G & 7
+    x, i = lin & 7, lin >> 3
+    n = q + 1 if x < rem else q
+    start = x * (q + 1) if x < rem else rem * (q + 1) + (x - rem) * q
+    return start + (n - 1 - i)

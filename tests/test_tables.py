@@ -343,3 +343,18 @@ def test_narrow_shape_constants_match_kernels_cpu():
     assert const("kRowsWide") == ks.WIDE["rows"] and const("kRowsNarrow") == ks.NARROW["rows"]
     assert const("kInvColsWide") == ks.WIDE["inv_cols"] and const("kInvColsNarrow") == ks.NARROW["inv_cols"]
     assert const("kNarrowMaxBatch") == ks.NARROW_MAX_BATCH
+
+
+def test_xcd_remaps_are_bijections_with_shared_ranges_cpu():
+    """Both workgroup maps cover every logical id once, and give each XCD
+    the same contiguous range (the reverse map walks it from the end), for
+    grids of 1 to 301 slices of the band kernels and odd sizes."""
+    for G in (1, 7, 8, 9, 68, 1088, 4352, 68 * 301, 16 * 3 + 5):
+        fwd = [ks.xcd_remap(l, G) for l in range(G)]
+        rev = [ks.xcd_remap_reverse(l, G) for l in range(G)]
+        assert sorted(fwd) == list(range(G)) and sorted(rev) == list(range(G))
+        for x in range(8):
+            a = [fwd[l] for l in range(x, G, 8)]
+            b = [rev[l] for l in range(x, G, 8)]
+            assert a == sorted(a) and b == sorted(b, reverse=True) and sorted(a) == sorted(b)
+            assert not a or a == list(range(a[0], a[0] + len(a)))
