@@ -52,6 +52,9 @@ extern "C" int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const
                              float* coef_im, int layout, float* xs, float* work, int64_t batch,
                              hipStream_t stream) {
     if (!route || !x || !xs || !work) return FCQT_EARG;
+    // validate the band half before launching the FFT half
+    if (int e = check_band_args(tab, route, coef_re, coef_im, layout, batch)) return e;
+    if (!aligned(xs, 8)) return FCQT_EALIGN;
     if (int e = fcqt_packed_fft_fwd(tab, x, xs, work, batch, stream)) return e;
     return fcqt_route_bands(tab, route, xs, coef_re, coef_im, layout, batch, stream);
 }

@@ -217,6 +217,7 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
     load_records(rv, rec, task_id);
     const float2* xb = xs + (long)b * kXStride;
     const int4 td = tasks[task_id];
+    if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
 #define FCQT_ROUTE(M_) route_band<M_, LAYOUT>(td, task_id, b, batch, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
         case 32: FCQT_ROUTE(32); break;
@@ -244,6 +245,7 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
     int task_id, b;
     decode_task<true>(batch, task_id, b);
     const int4 td = tasks[task_id];
+    if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
 #define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT>(td, task_id, b, batch, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
         case 32: FCQT_SCATTER(32); break;
@@ -258,10 +260,16 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
 #undef FCQT_SCATTER
 }
 
-static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const float* cre, const float* cim,
-                           int layout, int64_t batch) {
+}  // namespace fcqt
+
+// Checks shared by the band launchers: the record table, the task table,
+// the coefficient span the descriptor declares against ncoef (a task table
+// reaching past the coefficient row is refused), the layout and alignments.
+int fcqt::check_band_args(const fcqt_tables* tab, const int32_t* rec, const float* cre, const float* cim,
+                          int layout, int64_t batch) {
     if (!tab || !rec || !cre || batch < 1 || batch > kMaxBatch) return FCQT_EARG;
     if (!tab->tasks || !tab->tw_stage || tab->ntasks < 1 || tab->ncoef < 1) return FCQT_EARG;
+    if (tab->coef_span < 1 || tab->coef_span > tab->ncoef) return FCQT_EARG;
     if ((int64_t)tab->ntasks * batch >= (int64_t)1 << 31) return FCQT_EARG;
     if (layout != FCQT_PLANAR && layout != FCQT_INTERLEAVED) return FCQT_EARG;
     if (layout == FCQT_PLANAR && !cim) return FCQT_EARG;
@@ -269,8 +277,6 @@ static int check_band_args(const fcqt_tables* tab, const int32_t* rec, const flo
     if (layout == FCQT_PLANAR ? (!aligned(cre, 4) || !aligned(cim, 4)) : !aligned(cre, 8)) return FCQT_EALIGN;
     return FCQT_OK;
 }
-
-}  // namespace fcqt
 
 using namespace fcqt;
 

@@ -16,6 +16,12 @@ constexpr int64_t kMaxBatch = 1 << 22;
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// Checks shared by the band launchers (FCQT_OK, FCQT_EARG or FCQT_EALIGN):
+// record and task tables, the descriptor's coefficient span against ncoef,
+// layout, alignment; defined in bands.hip.
+int check_band_args(const fcqt_tables* tab, const int32_t* rec, const float* cre, const float* cim, int layout,
+                    int64_t batch);
+
 // Text of the last failed launch on this host thread.
 inline char* last_error_buf() {
     static thread_local char buf[256] = {0};

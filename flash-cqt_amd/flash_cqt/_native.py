@@ -12,7 +12,7 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 PLANAR = 0
 INTERLEAVED = 1
 
@@ -28,7 +28,7 @@ class Tables(ctypes.Structure):
     """Mirror of struct fcqt_tables."""
     _fields_ = [("tw_pass", ctypes.c_void_p), ("tw_half", ctypes.c_void_p),
                 ("tw_stage", ctypes.c_void_p), ("tasks", ctypes.c_void_p),
-                ("ntasks", ctypes.c_int32), ("ncoef", ctypes.c_int64)]
+                ("ntasks", ctypes.c_int32), ("ncoef", ctypes.c_int64), ("coef_span", ctypes.c_int64)]
 
 
 class NativeError(RuntimeError):

@@ -66,7 +66,7 @@ class FusedOctCQT:
         self._ct = _native.Tables(
             tw_pass=tb["tw_pass"].data_ptr(), tw_half=tb["tw_half"].data_ptr(),
             tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(),
-            ntasks=int(tb["tasks"].shape[0]), ncoef=int(self.ncoef))
+            ntasks=int(tb["tasks"].shape[0]), ncoef=int(self.ncoef), coef_span=int(built["coef_span"]))
         self._tp = {k: v.data_ptr() for k, v in tb.items()}
         # the reference exposes its band-engine tables as .radix (fused.py:430);
         # here the same name holds this engine's tables (formats in tables.py)
@@ -77,19 +77,32 @@ class FusedOctCQT:
     # ------------------------------------------------------------ buffers
 
     def _workspace(self, B):
-        """Per-batch-size buffers. Each scatter table gets its own half-spectrum
-        slot buffer (F for synthesis, FA for the analysis adjoint), zeroed once:
-        the slots a table never writes must stay zero."""
+        """Per-batch-size buffers of fwd/bwd: X, W, F (the synthesis scatter
+        buffer, zeroed once: the slots its table never writes must stay
+        zero), the coefficient planes and the output. The analysis adjoint's
+        own scatter buffer FA is added by fa_buffer, only when an adjoint
+        runs, so inference never holds it."""
         if B not in self._ws:
             with torch.cuda.device(self.dev):
                 e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)
                 z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
-                self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=z(B, T.FROW, 2), FA=z(B, T.FROW, 2),
+                self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=z(B, T.FROW, 2),
                                    KR=z(B, self.ncoef), KI=z(B, self.ncoef), XO=z(B, N))
             self._wp[B] = {k: v.data_ptr() for k, v in self._ws[B].items()}
         return self._ws[B]
 
-    _FBUF = {"scat": "F", "scat_a": "FA"}
+    def fa_buffer(self, B):
+        """The analysis-adjoint scatter buffer for batch B, allocated and
+        zeroed on first use (it belongs to the scat_a table only)."""
+        w = self._workspace(B)
+        if "FA" not in w:
+            with torch.cuda.device(self.dev):
+                w["FA"] = torch.zeros(B, T.FROW, 2, dtype=torch.float32, device=self.dev)
+            self._wp[B]["FA"] = w["FA"].data_ptr()
+        return w["FA"]
+
+    def _fbuf(self, table, B):
+        return self._workspace(B)["F"] if table == "scat" else self.fa_buffer(B)
 
     def _check_x(self, x):
         if x.dim() != 2 or x.shape[1] != N or x.shape[0] < 1:
@@ -178,7 +191,7 @@ class FusedOctCQT:
         w = self._workspace(B)
         _native.check(self.lib.fcqt_synthesis(self._ct, _native.ptr(self.tables[table]),
                                               _native.ptr(self.tables["ovf_" + table]), _native.ptr(c_re),
-                                              _native.ptr(c_im), layout, _native.ptr(w[self._FBUF[table]]),
+                                              _native.ptr(c_im), layout, _native.ptr(self._fbuf(table, B)),
                                               _native.ptr(w["W"]), _native.ptr(y), B,
                                               _native.stream_handle(self.dev.index)), "synthesis")
 

@@ -65,8 +65,11 @@ class SlicedCQT:
         self.oct_bins = oct_.oct_bins
         self.size_per_oct = oct_.size_per_oct
         self.frqs_hz = oct_.frqs_hz
+        # 'auto' takes the fp32 HIP engine only for fp32 on a GPU at the fused
+        # slice length; other dtypes keep the torch engine (which computes in
+        # the requested precision, as the reference's OctCQT does)
         use_hip = engine == "hip" or (engine == "auto" and self.device.type == "cuda"
-                                      and sl_len == 65536)
+                                      and sl_len == 65536 and dtype == torch.float32)
         if engine not in ("auto", "hip", "torch"):
             raise ValueError("engine must be 'auto', 'hip' or 'torch'")
         if use_hip:
@@ -197,16 +200,25 @@ class SlicedCQT:
         return self.__dict__["_fused_ws"], self.__dict__["_stream_ptr_cache"]
 
     def _ws(self, f, nsig, S):
-        """Engine buffers per (signals, slices per call); F is zeroed once."""
-        cache = self._caches(f)[0]
-        key = (nsig, S)
-        if key not in cache:
+        """Engine buffers for nsig * S slice rows. There is one buffer set per
+        engine, sized to the largest row count seen so far; a smaller call
+        uses its leading rows. Rows are independent, and F is only ever used
+        with the synthesis scatter table, so the slots that table never
+        writes stay zero in every row (F is zeroed when allocated). Memory is
+        therefore bounded by the largest call, whatever the signal lengths."""
+        cache, ptrs = self._caches(f)
+        B = nsig * S
+        full = cache.get("rows")
+        if full is None or full["B"] < B:
             from . import tables as T
-            B = nsig * S
             dev = f.dev
-            cache[key] = dict(X=torch.empty(B, T.XSTRIDE, 2, device=dev), W=torch.empty(B, T.L, 2, device=dev),
-                              F=torch.zeros(B, T.FROW, 2, device=dev), Y=torch.empty(B, self.sl_len, device=dev))
-        return cache[key]
+            cache.clear()
+            ptrs.clear()                 # cached raw pointers refer to the old buffers
+            cache["rows"] = full = dict(B=B, X=torch.empty(B, T.XSTRIDE, 2, device=dev),
+                                        W=torch.empty(B, T.L, 2, device=dev),
+                                        F=torch.zeros(B, T.FROW, 2, device=dev),
+                                        Y=torch.empty(B, self.sl_len, device=dev))
+        return {k: v[:B] for k, v in full.items() if k != "B"}
 
     def _tw32(self):
         tw = self.__dict__.get("_tw32_cache")

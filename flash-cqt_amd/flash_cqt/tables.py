@@ -240,7 +240,13 @@ def build(groups, nn=N, noct=None):
                 slice_groups=slice_groups(tasks, gspec, len(groups) - 2 if noct is None else noct),
                 ovf_scat=ovf, ovf_scat_a=ovf_a,
                 tw_pass=pass_twiddles(), tw_half=half_twiddles(), tw_stage=stage_twiddles(),
-                gspec=gspec, ncoef=ncoef)
+                gspec=gspec, ncoef=ncoef, coef_span=coef_span(tasks))
+
+
+def coef_span(tasks):
+    """One past the last coefficient any task touches (the C descriptor's
+    coef_span: launches are refused unless it is at most ncoef)."""
+    return int(max(int(t[1]) + int(t[2]) * int(t[0]) for t in np.asarray(tasks)))
 
 
 def scatter_table(bins, gr, gi):

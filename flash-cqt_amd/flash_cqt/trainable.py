@@ -53,7 +53,7 @@ class TrainableCQT:
     def _launch_synthesis(self, kc, table, fbuf):
         B = kc.shape[0]
         f = self.f
-        f._workspace(B)
+        f._fbuf(table, B)                  # the table's scatter buffer (FA on first adjoint use)
         p = f._wp[B]
         y = torch.empty(B, N, dtype=torch.float32, device=self.dev)
         _native.check(f.lib.fcqt_synthesis(f._ct, f._tp[table], f._tp["ovf_" + table], kc.data_ptr(), None,

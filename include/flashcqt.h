@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 6
+#define FCQT_ABI_VERSION 7
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -68,6 +68,10 @@ typedef struct fcqt_tables {
     const int32_t* tasks;     /* [ntasks][4] band tasks: M, first coefficient, band count, first band */
     int32_t        ntasks;
     int64_t        ncoef;     /* complex coefficients per slice (132992 for [3,4,2]/[8,16,32]) */
+    int64_t        coef_span; /* one past the last coefficient any task touches (the task table's
+                                 coverage, max of first + count * M); every band launch is refused
+                                 with FCQT_EARG unless 1 <= coef_span <= ncoef, and a task whose
+                                 coefficients reach past ncoef is skipped by the kernels */
 } fcqt_tables;
 
 /* ABI version of the loaded library (FCQT_ABI_VERSION). */

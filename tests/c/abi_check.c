@@ -25,6 +25,7 @@ int main(void) {
     tab.tasks = (const int32_t*)buf;
     tab.ntasks = 1;
     tab.ncoef = 1;
+    tab.coef_span = 1;
     hipStream_t s = 0;
 
     CHECK(fcqt_abi_version() == FCQT_ABI_VERSION);
@@ -38,6 +39,12 @@ int main(void) {
     CHECK(fcqt_route_bands(&tab, (const int32_t*)buf, buf, buf, buf, 7, 1, s) == FCQT_EARG);
     CHECK(fcqt_scatter_bands(&tab, (const int32_t*)buf, buf, buf, FCQT_PLANAR, NULL, 1, s) == FCQT_EARG);
     CHECK(fcqt_packed_fft_inv(&tab, NULL, buf, buf, buf, 1, s) == FCQT_EARG);
+    /* a task table reaching past the coefficient row is refused */
+    tab.coef_span = 2;
+    CHECK(fcqt_route_bands(&tab, (const int32_t*)buf, buf, buf, buf, FCQT_PLANAR, 1, s) == FCQT_EARG);
+    CHECK(fcqt_scatter_bands(&tab, (const int32_t*)buf, buf, buf, FCQT_PLANAR, buf, 1, s) == FCQT_EARG);
+    CHECK(fcqt_analysis(&tab, (const int32_t*)buf, buf, buf, buf, FCQT_PLANAR, buf, buf, 1, s) == FCQT_EARG);
+    tab.coef_span = 1;
     CHECK(fcqt_fill_zero(NULL, 4, s) == FCQT_EARG);
     CHECK(fcqt_fill_zero(buf, 0, s) == FCQT_OK);
     CHECK(fcqt_stream_overlap(buf, NULL, buf, 1, 1, s) == FCQT_EARG);

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 6
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 7
 
 
 def test_status_strings(lib):
@@ -43,8 +43,8 @@ def test_status_strings(lib):
 
 def test_argument_errors_detected_before_any_launch(lib):
     from flash_cqt._native import Tables
-    tab = Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=1, ncoef=1)
-    bad = Tables(tw_pass=0, tw_half=0, tw_stage=0, tasks=0, ntasks=0, ncoef=0)
+    tab = Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=1, ncoef=1, coef_span=1)
+    bad = Tables(tw_pass=0, tw_half=0, tw_stage=0, tasks=0, ntasks=0, ncoef=0, coef_span=0)
     s = ctypes.c_void_p(0)
     p = ctypes.c_void_p(4096)
     odd = ctypes.c_void_p(4100)
@@ -84,6 +84,33 @@ def test_argument_errors_detected_before_any_launch(lib):
     assert lib.fcqt_overlap_add(p, p, 1, 1, 2 * 32768 + 1, s) == EARG      # longer than nslices * 2H
     assert lib.fcqt_overlap_add(p, null, 1, 1, 10, s) == EARG
     assert lib.fcqt_fill_zero(p, 0, s) == 0  # nothing to do, no launch
+
+
+def test_coefficient_span_beyond_ncoef_is_refused(lib):
+    """A descriptor whose task table reaches past the coefficient row (ncoef
+    below the tasks' coverage), or that declares no coverage, is refused by
+    every band entry point before any launch (the compositions included:
+    fcqt_analysis checks its band half before launching its FFT half)."""
+    from flash_cqt._native import Tables
+    p = ctypes.c_void_p(4096)
+    s = ctypes.c_void_p(0)
+    for span, ncoef in ((132992, 132991), (0, 132992), (-5, 10)):
+        tab = ctypes.byref(Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=68, ncoef=ncoef,
+                                  coef_span=span))
+        assert lib.fcqt_route_bands(tab, p, p, p, p, 0, 1, s) == 1
+        assert lib.fcqt_route_bands_sliced(tab, p, p, p, p, 1, 1, 0, s) == 1
+        assert lib.fcqt_scatter_bands(tab, p, p, p, 0, p, 1, s) == 1
+        assert lib.fcqt_scatter_bands_sliced(tab, p, p, p, p, 1, 1, 0, s) == 1
+        assert lib.fcqt_analysis(tab, p, p, p, p, 0, p, p, 1, s) == 1
+        assert lib.fcqt_synthesis(tab, p, p, p, p, 0, p, p, p, 1, s) == 1
+
+
+def test_package_descriptor_declares_the_task_coverage(factored_tables):
+    """The table builder's coef_span is the task table's coverage, equal to
+    ncoef for the [3,4,2]/[8,16,32] layout."""
+    t = factored_tables
+    cov = max(int(f) + int(nb) * int(M) for M, f, nb, _ in t["tasks"].tolist())
+    assert t["coef_span"] == cov == t["ncoef"]
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -20,4 +20,4 @@ def test_header_from_c(tmp_path):
     assert r.returncode == 0, r.stderr
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
-    assert "c abi check ok (ABI 6)" in r.stdout
+    assert "c abi check ok (ABI 7)" in r.stdout
