@@ -275,11 +275,38 @@ def cpu_baseline(batch=64, budget_s=10.0, budget_b1_s=4.0, max_reps=400):
     """The reference OctCQT algorithm (oracle torch port) on the host cores,
     on a bounded sample of the bench's own workload (batch-`batch` round trips
     of the randn input, about budget_s of CPU work), plus batch 1 on the
-    configs[1] input and batches 4 and 16 on randn input (short samples)."""
+    configs[1] input and batches 4 and 16 on randn input (short samples).
+    torch runs with os.cpu_count() threads, as the survey's measurement
+    specifies; the CPUs this process may run on (affinity) and the cgroup CPU
+    quota are reported beside it. The previous thread count is restored."""
     from oracle.torch_port import TorchPortOctCQT
-    cores = min(os.cpu_count() or 1, 16)
+    cores = os.cpu_count() or 1
+    prev_threads = torch.get_num_threads()
     torch.set_num_threads(cores)
-    port = TorchPortOctCQT()
+    try:
+        return _cpu_baseline(TorchPortOctCQT(), cores, batch, budget_s, budget_b1_s, max_reps)
+    finally:
+        torch.set_num_threads(prev_threads)
+
+
+def host_cpus():
+    """CPUs this process may run on, and the cgroup v2 quota in CPUs (None
+    if unlimited or unreadable)."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    quota = None
+    try:
+        q, per = pathlib.Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = int(q) / int(per)
+    except (OSError, ValueError):
+        pass
+    return affinity, quota
+
+
+def _cpu_baseline(port, cores, batch, budget_s, budget_b1_s, max_reps):
 
     def timed(x, budget):
         with torch.no_grad():
@@ -310,13 +337,56 @@ def cpu_baseline(batch=64, budget_s=10.0, budget_b1_s=4.0, max_reps=400):
                     break
     except OSError:
         pass
+    affinity, quota = host_cpus()
     return {"value": batch / med, "unit": "slice round trips/s", "cores": cores, "kind": "port",
+            "cpu_model": model, "cpus_in_affinity": affinity, "cgroup_cpu_quota": quota,
             "sample": f"{n} batch-{batch} round trips of the bench's randn input (median {med * 1e3:.1f} ms "
-                      f"per batch), oracle/torch_port.py, torch CPU {cores} threads, {model}",
+                      f"per batch), oracle/torch_port.py, torch CPU {cores} threads (os.cpu_count(); "
+                      f"{affinity} CPUs in this process's affinity, cgroup quota {quota} CPUs), {model}",
             "snr_db": db,
             "batch1": {"value": 1.0 / med1, "sample": f"{n1} batch-1 round trips of the configs[1] input "
                                                      f"(median {med1 * 1e3:.2f} ms)", "snr_db": db1},
             "per_batch": per_batch}
+
+
+# ------------------------------------------------------------ peak memory
+
+def peak_mb(fn):
+    """Peak device memory one call allocates beyond what was allocated
+    before it, in MB (the reference's recipe, bench/memory_bars.py:24-31)."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    fn()
+    torch.cuda.synchronize()
+    return (torch.cuda.max_memory_allocated() - base) / 1e6
+
+
+def peak_memory(cqt_gpu, dev, batches=(1, 8, 16, 32, 64, 128)):
+    """Peak MB of one round-trip call per batch size, every buffer the call
+    needs allocated inside it (a fresh engine with resident tables: the
+    first call of a batch size allocates X, W, F, the coefficient planes
+    and the output), beside the hipFFT-call baseline (pure-torch OctCQT)
+    measured the same way. The reference publishes 2.6 / 21.1 / 84.4 /
+    337.5 MB at batches 1 / 8 / 32 / 128 (bench/figure.py:21-23)."""
+    from flash_cqt.fused import FusedOctCQT
+    f = FusedOctCQT(cqt_gpu, dev)
+    out = {}
+    for B in batches:
+        x = randn(B, 2).to(dev)
+        with torch.no_grad():
+            ours = peak_mb(lambda: f.bwd(*f.fwd(x)))
+            lib = peak_mb(lambda: cqt_gpu.bwd(*cqt_gpu.fwd(x)))
+        out[str(B)] = {"peak_mb": ours, "peak_mb_per_slice": ours / B, "hipfft_baseline_peak_mb": lib}
+        f._ws.pop(B, None)
+        f._wp.pop(B, None)
+    table_mb = sum(f.table_bytes.values()) / 1e6
+    log("peak MB per round-trip call: " + "  ".join(f"B={b}: {v['peak_mb']:.1f} (hipFFT {v['hipfft_baseline_peak_mb']:.1f})"
+                                                    for b, v in out.items()) + f"; tables resident {table_mb:.1f} MB")
+    return {"per_batch": out, "tables_resident_mb": table_mb,
+            "method": "torch.cuda.max_memory_allocated minus the allocation before one round-trip call whose "
+                      "buffers are all allocated inside it (fresh engine per batch size, tables resident)"}
 
 
 # ---------------------------------------------------------- kernel timings
@@ -554,8 +624,21 @@ def main():
                                "launches, median of 7 runs",
             "ms_per_launch_graph": kern[dom]["ms_per_call_graph"] / kern[dom]["launches"]}
 
+    # the whole round trip against the same peak: algorithmic bytes of the
+    # timed step over its duration, and the HBM traffic the six kernels
+    # move per round trip (committed counter summary, batch 64)
+    rt_traffic = None
+    if B == 64:
+        parts = [measured_traffic(k, B) for k in KERNEL_SYMBOL]
+        if all(t is not None for t in parts):
+            rt_traffic = sum(t * KERNEL_LAUNCHES[k] for t, k in zip(parts, KERNEL_SYMBOL))
+    roof_rt = {"bound": "hbm", "achieved": gbps, "peak": PEAK_GBPS, "unit": "GB/s", "frac": gbps / PEAK_GBPS,
+               "traffic": rt_traffic, "alg_bytes_per_step": B * SLICE_RT_BYTES, "ms_per_step": ms_step,
+               "traffic_source": "sum over the six kernels in profiles/hbm_traffic_b64.txt" if rt_traffic else None}
+
     sliced = sliced_workload(dev)
     train = training_step(dev, cqt_gpu)
+    mem = peak_memory(cqt_gpu, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(batch=B)
 
     line = {
@@ -576,6 +659,8 @@ def main():
         "training_step": train,
         "table_bytes": f.table_bytes,
         "roofline": roof,
+        "roofline_roundtrip": roof_rt,
+        "peak_memory": mem,
         "cpu_baseline": cpu,
     }
     print(json.dumps(json_safe(line)), flush=True)

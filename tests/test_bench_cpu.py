@@ -32,11 +32,17 @@ def test_json_safe_is_strict(bench):
 
 
 def test_cpu_baseline_contract(bench):
-    """kind "port", the threads used, a sample description, the batch-64
-    value plus batches 1, 4 and 16 (run here at batch 2 on a tiny budget)."""
+    """kind "port", os.cpu_count() threads (uncapped, restored afterwards),
+    the CPU model and affinity, a sample description, the batch-64 value
+    plus batches 1, 4 and 16 (run here at batch 2 on a tiny budget)."""
+    import os
+    import torch
+    before = torch.get_num_threads()
     cb = bench.cpu_baseline(batch=2, budget_s=0.01, budget_b1_s=0.01, max_reps=1)
+    assert torch.get_num_threads() == before
     assert cb["kind"] == "port" and cb["unit"] == "slice round trips/s"
-    assert cb["cores"] >= 1 and cb["value"] > 0 and "round trips" in cb["sample"]
+    assert cb["cores"] == os.cpu_count() and cb["value"] > 0 and "round trips" in cb["sample"]
+    assert "cpus_in_affinity" in cb and "cpu_model" in cb
     assert set(cb["per_batch"]) == {"1", "2", "4", "16"}
     assert cb["snr_db"] > 125 and cb["batch1"]["snr_db"] > 125
     assert all(math.isfinite(v["round_trips_per_s"]) for v in cb["per_batch"].values())

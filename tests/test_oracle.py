@@ -200,3 +200,47 @@ def test_sliced_matches_reference(golden):
     y = s.bwd(bl, sd, length=x.shape[-1])
     assert co.snr_db(golden["sliced_bwd_sub"], y[..., ::st]) > 120
     assert co.snr_db(x, y) > 135
+
+
+# ------------------------------------------------------- host-core baseline
+
+def test_torch_port_matches_oracle_and_reference(oracle, golden):
+    """oracle/torch_port.py is what bench.py times as the host-core
+    baseline: it must compute the same transform. Forward coefficients and
+    the inverse (with and without the side bands) against the float64
+    oracle at >= 120 dB, and against the reference's golden vectors."""
+    import torch
+    from oracle.torch_port import TorchPortOctCQT
+    port = TorchPortOctCQT()
+    x, _ = inputs()
+    with torch.no_grad():
+        pb, ps = port.fwd(torch.from_numpy(x))
+        got = np.concatenate([c.numpy().reshape(x.shape[0], -1) for c in list(pb) + list(ps)], -1)
+        bl, sd = oracle.fwd(x)
+        ref = oracle.flatten(bl, sd)
+        assert co.snr_db(ref, got) >= 120
+        st = int(golden["meta_stride"][0])
+        assert co.snr_db(golden["fwd_sub"], got[:, ::st]) >= 120
+        # the inverse on the oracle's coefficients (rounded to complex64)
+        c64 = [torch.from_numpy(c.astype(np.complex64)) for c in list(bl) + list(sd)]
+        y = port.bwd(c64[:len(bl)], c64[len(bl):]).numpy()
+        assert co.snr_db(oracle.bwd(bl, sd), y) >= 120
+        assert co.snr_db(golden["bwd_sub"], y[:, ::st]) >= 120
+        # round trip of the port alone
+        assert co.snr_db(x, port.bwd(pb, ps).numpy()) >= 125
+
+
+def test_planted_port_mistake_is_caught(oracle):
+    """A plausible slip in the port (the dual window of one group left out of
+    the inverse) must fail the comparison above."""
+    import torch
+    from oracle.torch_port import TorchPortOctCQT
+    port = TorchPortOctCQT()
+    idx, gv, pos, gdv, conj = port.groups[3]
+    port.groups[3] = (idx, gv, pos, torch.ones_like(gdv), conj)
+    x, _ = inputs()
+    bl, sd = oracle.fwd(x)
+    c64 = [torch.from_numpy(c.astype(np.complex64)) for c in list(bl) + list(sd)]
+    with torch.no_grad():
+        y = port.bwd(c64[:len(bl)], c64[len(bl):]).numpy()
+    assert co.snr_db(oracle.bwd(bl, sd), y) < 60
