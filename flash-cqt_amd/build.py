@@ -22,7 +22,7 @@ import sys
 ROOT = pathlib.Path(__file__).resolve().parent
 CSRC = ROOT / "csrc"
 OUT = ROOT / "flash_cqt" / "_lib" / "libflashcqt.so"
-SOURCES = ("abi.hip", "bands.hip", "packed_fft.hip")
+SOURCES = ("abi.hip", "bands.hip", "packed_fft.hip", "image.hip")
 ARCH = "gfx950"
 
 

@@ -21,7 +21,8 @@ EXPORTS = ("fcqt_abi_version", "fcqt_status_string", "fcqt_last_hip_error",
            "fcqt_packed_fft_fwd", "fcqt_route_bands", "fcqt_scatter_bands",
            "fcqt_packed_fft_inv", "fcqt_analysis", "fcqt_synthesis", "fcqt_fill_zero",
            "fcqt_slice_fft_fwd", "fcqt_route_bands_sliced", "fcqt_scatter_bands_sliced",
-           "fcqt_overlap_add", "fcqt_stream_overlap")
+           "fcqt_overlap_add", "fcqt_stream_overlap", "fcqt_image_check", "fcqt_tables_upload",
+           "fcqt_workspace_sizes")
 
 
 class Tables(ctypes.Structure):
@@ -29,6 +30,24 @@ class Tables(ctypes.Structure):
     _fields_ = [("tw_pass", ctypes.c_void_p), ("tw_half", ctypes.c_void_p),
                 ("tw_stage", ctypes.c_void_p), ("tasks", ctypes.c_void_p),
                 ("ntasks", ctypes.c_int32), ("ncoef", ctypes.c_int64), ("coef_span", ctypes.c_int64)]
+
+
+class ImageInfo(ctypes.Structure):
+    """Mirror of struct fcqt_image_info."""
+    _fields_ = [("device_bytes", ctypes.c_int64), ("ncoef", ctypes.c_int64), ("coef_span", ctypes.c_int64),
+                ("ntasks", ctypes.c_int32), ("format", ctypes.c_int32)]
+
+
+class EngineTables(ctypes.Structure):
+    """Mirror of struct fcqt_engine_tables."""
+    _fields_ = [("tab", Tables)] + [(n, ctypes.c_void_p) for n in
+                                    ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a",
+                                     "slice_groups")]
+
+
+class Sizes(ctypes.Structure):
+    """Mirror of struct fcqt_sizes."""
+    _fields_ = [(n, ctypes.c_int64) for n in ("signal", "spectrum", "work", "scatter", "coef_plane", "tail")]
 
 
 class NativeError(RuntimeError):
@@ -68,6 +87,9 @@ def load():
         "fcqt_scatter_bands_sliced": ([T, P, P, P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_overlap_add": ([P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_stream_overlap": ([P, P, P, I64, I64, S], ctypes.c_int),
+        "fcqt_image_check": ([ctypes.c_char_p, I64, ctypes.POINTER(ImageInfo)], ctypes.c_int),
+        "fcqt_tables_upload": ([ctypes.c_char_p, I64, P, I64, S, ctypes.POINTER(EngineTables)], ctypes.c_int),
+        "fcqt_workspace_sizes": ([T, I64, ctypes.POINTER(Sizes)], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

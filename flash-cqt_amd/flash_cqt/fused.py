@@ -56,18 +56,33 @@ class FusedOctCQT:
         built = T.build(_np_groups(cqt), noct=len(cqt.groups))
         self.gspec = built["gspec"]
         self.ncoef = built["ncoef"]
+        # the tables go to the device as one table image through the C ABI's
+        # checked upload (fcqt_tables_upload validates every record against
+        # the kernels' bounds on the host first), into one device buffer
+        image = T.image_bytes(built)
+        info = _native.ImageInfo()
+        _native.check(self.lib.fcqt_image_check(image, len(image), info), "image_check")
+        with torch.cuda.device(dev):
+            self._table_mem = torch.empty(info.device_bytes, dtype=torch.uint8, device=dev)
+            up = _native.EngineTables()
+            _native.check(self.lib.fcqt_tables_upload(image, len(image), self._table_mem.data_ptr(), info.device_bytes,
+                                                      _native.stream_handle(dev.index), up), "tables_upload")
+        self._up = up
+        self._ct = up.tab
+        assert self._ct.ncoef == self.ncoef and self._ct.coef_span == built["coef_span"]
+        # per-table tensor views of the uploaded image (same device memory)
         self.tables = {}
-        for name in ("route", "route_b", "scat", "scat_a", "ovf_scat", "ovf_scat_a", "tasks", "slice_groups",
-                     "tw_pass", "tw_half", "tw_stage"):
-            self.tables[name] = torch.as_tensor(np.ascontiguousarray(built[name])).to(dev)
+        for _, (name, dt) in T.IMAGE_SECTIONS.items():
+            if name == "ncoef":
+                continue
+            ptr = getattr(up, name) if hasattr(up, name) else getattr(up.tab, name)
+            a = np.asarray(built[name], dtype=dt)
+            off = ptr - self._table_mem.data_ptr()
+            tdt = torch.float32 if dt == np.float32 else torch.int32
+            self.tables[name] = self._table_mem[off:off + a.nbytes].view(tdt).view(a.shape)
         # table bytes per direction (batch invariant, L2/MALL resident at batch)
         self.table_bytes = {k: v.numel() * v.element_size() for k, v in self.tables.items()}
-        tb = self.tables
-        self._ct = _native.Tables(
-            tw_pass=tb["tw_pass"].data_ptr(), tw_half=tb["tw_half"].data_ptr(),
-            tw_stage=tb["tw_stage"].data_ptr(), tasks=tb["tasks"].data_ptr(),
-            ntasks=int(tb["tasks"].shape[0]), ncoef=int(self.ncoef), coef_span=int(built["coef_span"]))
-        self._tp = {k: v.data_ptr() for k, v in tb.items()}
+        self._tp = {k: v.data_ptr() for k, v in self.tables.items()}
         # the reference exposes its band-engine tables as .radix (fused.py:430);
         # here the same name holds this engine's tables (formats in tables.py)
         self.radix = self.tables

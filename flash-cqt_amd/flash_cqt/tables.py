@@ -352,3 +352,56 @@ def check_band_taps(bands, groups, nn=N):
             assert np.array_equal(cj[live], conj[i][live])
             assert not np.any((k < 0) & live)
             bi += 1
+
+
+# ------------------------------------------------------------ table image
+# A flat, versioned image of every batch-invariant table, for callers of the
+# C ABI that do not run Python at load time: write it once here
+# (image_bytes / save_image), then fcqt_image_check validates it on the host
+# and fcqt_tables_upload copies it into caller-allocated device memory and
+# fills the descriptors (include/flashcqt.h). Layout, little endian:
+#   header   "FCQT", u32 format version, u32 section count, u32 0
+#   sections u32 id, u32 element bytes, u64 element count, u64 byte offset
+#   data     each section at a 256-byte aligned offset from the image start
+# The device copy keeps the same offsets, so a table's device address is
+# the device base plus its offset.
+
+IMAGE_MAGIC = b"FCQT"
+IMAGE_VERSION = 1
+IMAGE_ALIGN = 256
+# section id -> (name in build(), element type)
+IMAGE_SECTIONS = {
+    1: ("tw_pass", np.float32), 2: ("tw_half", np.float32), 3: ("tw_stage", np.float32),
+    4: ("tasks", np.int32), 5: ("route", np.int32), 6: ("route_b", np.int32),
+    7: ("scat", np.int32), 8: ("scat_a", np.int32), 9: ("ovf_scat", np.int32),
+    10: ("ovf_scat_a", np.int32), 11: ("slice_groups", np.int32), 12: ("ncoef", np.int64),
+}
+
+
+def image_bytes(built):
+    """The table image of build()'s output, as bytes."""
+    import struct
+    arrays = []
+    for sid, (name, dt) in IMAGE_SECTIONS.items():
+        v = built[name]
+        a = np.asarray([v] if np.ndim(v) == 0 else v, dtype=dt).reshape(-1)
+        arrays.append((sid, np.ascontiguousarray(a)))
+    head = 16 + 24 * len(arrays)
+    off = -(-head // IMAGE_ALIGN) * IMAGE_ALIGN
+    secs, blobs = [], []
+    for sid, a in arrays:
+        secs.append(struct.pack("<IIQQ", sid, a.itemsize, a.size, off))
+        blobs.append((off, a.tobytes()))
+        off += -(-a.nbytes // IMAGE_ALIGN) * IMAGE_ALIGN
+    out = bytearray(off)
+    out[:16] = IMAGE_MAGIC + struct.pack("<III", IMAGE_VERSION, len(arrays), 0)
+    out[16:head] = b"".join(secs)
+    for o, b in blobs:
+        out[o:o + len(b)] = b
+    return bytes(out)
+
+
+def save_image(built, path):
+    """Write build()'s tables as a table image file."""
+    with open(path, "wb") as f:
+        f.write(image_bytes(built))

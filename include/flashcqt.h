@@ -74,6 +74,71 @@ typedef struct fcqt_tables {
                                  coefficients reach past ncoef is skipped by the kernels */
 } fcqt_tables;
 
+/* ---- table image, upload and buffer sizes ----
+ * The batch-invariant tables come from the host builder
+ * (flash-cqt_amd/flash_cqt/tables.py: build() computes them in float64 from
+ * the OctCQT bank, image_bytes()/save_image() write them as one flat image);
+ * the library does not compute tables. A C or C++ caller loads an image
+ * file once, checks it, uploads it and sizes its buffers with the three
+ * calls below; no Python is needed at run time. */
+
+#define FCQT_IMAGE_VERSION 1  /* table image format understood by this library */
+
+/* What a checked image holds. */
+typedef struct fcqt_image_info {
+    int64_t device_bytes;   /* device bytes fcqt_tables_upload needs (the image length) */
+    int64_t ncoef;          /* complex coefficients per slice */
+    int64_t coef_span;      /* the task table's coverage (== ncoef for a consistent image) */
+    int32_t ntasks;         /* band tasks */
+    int32_t format;         /* image format version */
+} fcqt_image_info;
+
+/* Descriptors of an uploaded image: every table the entry points take. */
+typedef struct fcqt_engine_tables {
+    fcqt_tables    tab;           /* twiddles, tasks, ncoef, coef_span */
+    const int32_t* route;         /* analysis route records */
+    const int32_t* route_b;       /* synthesis-adjoint route records */
+    const int32_t* scat;          /* synthesis scatter records */
+    const int32_t* scat_a;        /* analysis-adjoint scatter records */
+    const int32_t* ovf_scat;      /* fold lists of scat */
+    const int32_t* ovf_scat_a;    /* fold lists of scat_a */
+    const int32_t* slice_groups;  /* SlicedCQT group records */
+} fcqt_engine_tables;
+
+/* Check a table image held in host memory, without any HIP call: the
+ * header and section table (ids, element sizes, counts, 256-byte aligned
+ * offsets inside the image), and every table against the bounds the kernels
+ * index with: band lengths and counts of the tasks, their coefficient
+ * coverage against ncoef, route bins <= 32768, scatter slots inside an F row
+ * and their gain modes, fold-list bins and overflow indices, slice-group
+ * records against their tasks. Fills *info (may be NULL) on success.
+ * Returns FCQT_OK or FCQT_EARG. No counterpart in the reference, whose
+ * tables are device tensors built in Python (fused.py:229-476). */
+int fcqt_image_check(const void* image, int64_t len, fcqt_image_info* info);
+
+/* Check the image (as fcqt_image_check), copy it into `dev`, caller-owned
+ * device memory of at least info.device_bytes bytes, 256-byte aligned, and
+ * fill *out with device pointers into it. The copy is enqueued on `stream`
+ * and waited for (hipStreamSynchronize), so the image may be freed on
+ * return: a set-up call, not for graph capture. Allocates nothing. */
+int fcqt_tables_upload(const void* image, int64_t len, void* dev, int64_t dev_bytes, hipStream_t stream,
+                       fcqt_engine_tables* out);
+
+/* Bytes of every caller-allocated buffer at a batch size. */
+typedef struct fcqt_sizes {
+    int64_t signal;      /* x or y: batch * 65536 fp32 */
+    int64_t spectrum;    /* xs: batch * FCQT_XSTRIDE complex */
+    int64_t work;        /* work: batch * 32768 complex */
+    int64_t scatter;     /* f, one per scatter table: batch * FCQT_FROW complex */
+    int64_t coef_plane;  /* one FCQT_PLANAR plane: batch * ncoef fp32 (FCQT_INTERLEAVED: twice this) */
+    int64_t tail;        /* fcqt_stream_overlap tail: batch (signals) * 32768 fp32 */
+} fcqt_sizes;
+
+/* Fill *out for `batch` slices (tab supplies ncoef). FCQT_EARG on a bad
+ * argument or a size that overflows. No counterpart in the reference (its
+ * callers size buffers from Python constants, trainable.py:75-110). */
+int fcqt_workspace_sizes(const fcqt_tables* tab, int64_t batch, fcqt_sizes* out);
+
 /* ABI version of the loaded library (FCQT_ABI_VERSION). */
 int fcqt_abi_version(void);
 

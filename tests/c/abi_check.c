@@ -1,8 +1,11 @@
 /* A C consumer of include/flashcqt.h: compiles as C99 against the header,
  * links libflashcqt.so and exercises the calls that need no GPU (version,
- * status strings, argument checks made before any HIP call). Exit 0 on
- * success; prints the first failed check otherwise. */
+ * status strings, argument checks made before any HIP call), then loads a
+ * table image file (argv[1], written by flash_cqt/tables.py save_image),
+ * checks it and sizes every buffer for batch 64 from the library alone.
+ * Exit 0 on success; prints the first failed check otherwise. */
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "flashcqt.h"
@@ -15,7 +18,7 @@
         }                                                             \
     } while (0)
 
-int main(void) {
+int main(int argc, char** argv) {
     static float buf[64] __attribute__((aligned(16)));
     fcqt_tables tab;
     memset(&tab, 0, sizeof(tab));
@@ -48,6 +51,32 @@ int main(void) {
     CHECK(fcqt_fill_zero(NULL, 4, s) == FCQT_EARG);
     CHECK(fcqt_fill_zero(buf, 0, s) == FCQT_OK);
     CHECK(fcqt_stream_overlap(buf, NULL, buf, 1, 1, s) == FCQT_EARG);
+    if (argc > 1) {
+        FILE* fp = fopen(argv[1], "rb");
+        CHECK(fp != NULL);
+        fseek(fp, 0, SEEK_END);
+        long len = ftell(fp);
+        fseek(fp, 0, SEEK_SET);
+        unsigned char* img = (unsigned char*)malloc((size_t)len);
+        CHECK(img != NULL && fread(img, 1, (size_t)len, fp) == (size_t)len);
+        fclose(fp);
+        fcqt_image_info info;
+        CHECK(fcqt_image_check(img, len, &info) == FCQT_OK);
+        CHECK(info.device_bytes == len && info.ncoef == info.coef_span && info.ntasks > 0);
+        img[0] = 'X';
+        CHECK(fcqt_image_check(img, len, NULL) == FCQT_EARG);
+        free(img);
+        fcqt_tables t2;
+        memset(&t2, 0, sizeof(t2));
+        t2.ncoef = info.ncoef;
+        fcqt_sizes sz;
+        CHECK(fcqt_workspace_sizes(&t2, 64, &sz) == FCQT_OK);
+        printf("image ok: %lld device bytes, ncoef %lld, %d tasks\n", (long long)info.device_bytes,
+               (long long)info.ncoef, (int)info.ntasks);
+        printf("batch 64 bytes: signal %lld spectrum %lld work %lld scatter %lld coef_plane %lld tail %lld\n",
+               (long long)sz.signal, (long long)sz.spectrum, (long long)sz.work, (long long)sz.scatter,
+               (long long)sz.coef_plane, (long long)sz.tail);
+    }
     printf("c abi check ok (ABI %d)\n", fcqt_abi_version());
     return 0;
 }

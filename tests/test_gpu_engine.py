@@ -661,3 +661,18 @@ def test_bad_inputs_rejected(fused):
         fused.bwd(kr, kr)
     with pytest.raises(ValueError):                              # wrong dtype
         fused.fwd(torch.zeros(1, N, device=_dev(), dtype=torch.float64))
+
+
+def test_uploaded_tables_equal_builder_arrays(fused, cqt_gpu):
+    """FusedOctCQT loads its tables through fcqt_tables_upload: every device
+    table (views into the one uploaded buffer) equals the host builder's
+    array bit for bit, and the descriptor carries ncoef and coef_span."""
+    from flash_cqt import tables as T
+    from flash_cqt.fused import _np_groups
+    built = T.build(_np_groups(cqt_gpu), noct=len(cqt_gpu.groups))
+    for _, (name, dt) in T.IMAGE_SECTIONS.items():
+        if name == "ncoef":
+            continue
+        got = fused.tables[name].cpu().numpy()
+        assert np.array_equal(got.view(np.uint8), np.ascontiguousarray(built[name], dtype=dt).view(np.uint8)), name
+    assert fused._ct.ncoef == built["ncoef"] == fused._ct.coef_span
