@@ -1,5 +1,7 @@
 // C-ABI entry points that compose the engines (analysis, synthesis), the
-// graph-safe zero fill and the status helpers.
+// allocation-free analysis, the graph-safe zero fill and the status helpers.
+#include <mutex>
+
 #include "fcqt_fft.hpp"
 #include "fcqt_abi_internal.hpp"
 
@@ -25,6 +27,7 @@ extern "C" const char* fcqt_status_string(int status) {
         case FCQT_EARG: return "invalid argument (null pointer, size or layout)";
         case FCQT_EALIGN: return "misaligned pointer";
         case FCQT_ELAUNCH: return "kernel launch failed";
+        case FCQT_ECAPACITY: return "batch exceeds the static scratch capacity (FCQT_STATIC_MAX_BATCH slices)";
         default: return "unknown status";
     }
 }
@@ -69,4 +72,65 @@ extern "C" int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const
     if (!aligned(f, 16) || !aligned(y, 8) || !aligned(work, 8) || !aligned(ovf, 4)) return FCQT_EALIGN;
     if (int e = fcqt_scatter_bands(tab, scat, coef_re, coef_im, layout, f, batch, stream)) return e;
     return fcqt_packed_fft_inv(tab, ovf, f, y, work, batch, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free analysis. The spectrum X and the four-step intermediate W
+// of up to FCQT_STATIC_MAX_BATCH slices live in this file-scope device array
+// (every GPU the library runs on holds its own copy until the process ends).
+// Both are fully overwritten by every call, so nothing needs clearing. Host
+// code never passes the array's name to a kernel: the device address of each
+// GPU's copy is looked up once per device (hipGetSymbolAddress, with that
+// device current) and that address is passed instead.
+namespace fcqt {
+
+constexpr int64_t kStaticXs = (int64_t)FCQT_STATIC_MAX_BATCH * kXStride;   // complex elements of X
+constexpr int64_t kStaticWork = (int64_t)FCQT_STATIC_MAX_BATCH * kL;      // complex elements of W
+static __device__ __align__(256) float2 scratch[kStaticXs + kStaticWork];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of this GPU's scratch (FCQT_OK), resolved on first use.
+static int scratch_address(int device, float2** out) {
+    static std::mutex mu;
+    static float2* addr[kMaxDevices] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            std::snprintf(last_error_buf(), 256, "hipGetSymbolAddress: %s (%d)", hipGetErrorString(e), (int)e);
+            return FCQT_ELAUNCH;
+        }
+        addr[device] = static_cast<float2*>(p);
+    }
+    *out = addr[device];
+    return FCQT_OK;
+}
+
+}  // namespace fcqt
+
+extern "C" int fcqt_analysis_static(const fcqt_tables* tab, const int32_t* route, const float* x, float* coef_re,
+                                    float* coef_im, int layout, int64_t batch, hipStream_t stream) {
+    if (!route || !x) return FCQT_EARG;
+    if (int e = check_band_args(tab, route, coef_re, coef_im, layout, batch)) return e;
+    if (!tab->tw_pass || !tab->tw_half) return FCQT_EARG;
+    if (batch > FCQT_STATIC_MAX_BATCH) return FCQT_ECAPACITY;
+    if (!aligned(x, 8) || !aligned(tab->tw_pass, 8) || !aligned(tab->tw_half, 8)) return FCQT_EALIGN;
+    // the scratch of the GPU the launches go to: the stream's device, which
+    // must be the current one (hipGetSymbolAddress resolves for it)
+    int cur = -1, dev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess) e = stream ? hipStreamGetDevice(stream, &dev) : (dev = cur, hipSuccess);
+    if (e != hipSuccess) {
+        std::snprintf(last_error_buf(), 256, "%s (%d)", hipGetErrorString(e), (int)e);
+        return FCQT_ELAUNCH;
+    }
+    if (dev != cur || dev < 0 || dev >= kMaxDevices) return FCQT_EARG;
+    float2* base = nullptr;
+    if (int r = scratch_address(dev, &base)) return r;
+    float* xs = reinterpret_cast<float*>(base);
+    float* work = reinterpret_cast<float*>(base + kStaticXs);
+    if (int r = fcqt_packed_fft_fwd(tab, x, xs, work, batch, stream)) return r;
+    return fcqt_route_bands(tab, route, xs, coef_re, coef_im, layout, batch, stream);
 }

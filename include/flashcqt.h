@@ -9,8 +9,10 @@
  *
  * Conventions
  *   - Every buffer is device memory allocated by the caller; the library
- *     never allocates or frees. Tables are built on the host (the Python
- *     package flash_cqt/tables.py) and uploaded by the caller.
+ *     never allocates or frees (fcqt_analysis_static keeps its workspace in
+ *     a static device array of the library instead). Tables are built on
+ *     the host (the Python package flash_cqt/tables.py) and uploaded by the
+ *     caller (fcqt_tables_upload).
  *   - Complex buffers are interleaved fp32 pairs (re, im), 8-byte aligned.
  *     Record tables (int32 quadruples) must be 16-byte aligned.
  *   - All work is enqueued asynchronously on `stream` (any HIP stream,
@@ -55,6 +57,7 @@ extern "C" {
 #define FCQT_EARG 1      /* null pointer, bad size or bad enum */
 #define FCQT_EALIGN 2    /* pointer misaligned for its element type */
 #define FCQT_ELAUNCH 3   /* kernel launch failed (HIP error) */
+#define FCQT_ECAPACITY 4 /* batch beyond the static scratch capacity of fcqt_analysis_static */
 
 /* coefficient layouts */
 #define FCQT_PLANAR 0       /* re and im in two [batch][ncoef] fp32 planes */
@@ -221,6 +224,22 @@ int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float*
 int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                   float* coef_re, float* coef_im, int layout,
                   float* xs, float* work, int64_t batch, hipStream_t stream);
+
+/* Allocation-free analysis: fcqt_analysis with the spectrum X and the work
+ * buffer taken from a static device array of the library (each GPU holds its
+ * own copy, FCQT_STATIC_MAX_BATCH slices = 8.4 MB, until the process ends),
+ * so a caller passes only x and the coefficient buffers. It makes no HIP
+ * allocation and calls no allocating routine. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * results as fcqt_analysis, bit for bit.
+ *   batch <= FCQT_STATIC_MAX_BATCH, else FCQT_ECAPACITY (nothing launched)
+ *   stream must belong to the current device (the default stream does)
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (unordered streams, other threads) race; order them on one stream. */
+#define FCQT_STATIC_MAX_BATCH 16
+int fcqt_analysis_static(const fcqt_tables* tab, const int32_t* route, const float* x,
+                         float* coef_re, float* coef_im, int layout, int64_t batch, hipStream_t stream);
 
 /* Synthesis in one call: fcqt_scatter_bands then fcqt_packed_fft_inv, with
  * the scatter table `scat` and its overflow map `ovf` (same F rules). */

@@ -105,6 +105,24 @@ def test_coefficient_span_beyond_ncoef_is_refused(lib):
         assert lib.fcqt_synthesis(tab, p, p, p, p, 0, p, p, p, 1, s) == 1
 
 
+def test_static_analysis_argument_errors_before_any_launch(lib):
+    """fcqt_analysis_static checks its arguments, and its batch against the
+    static scratch capacity (FCQT_ECAPACITY), before any HIP call."""
+    from flash_cqt._native import Tables
+    p = ctypes.c_void_p(4096)
+    s = ctypes.c_void_p(0)
+    tab = ctypes.byref(Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=68, ncoef=132992,
+                              coef_span=132992))
+    assert lib.fcqt_analysis_static(tab, p, p, p, p, 0, 17, s) == 4
+    assert b"capacity" in lib.fcqt_status_string(4)
+    assert lib.fcqt_analysis_static(tab, None, p, p, p, 0, 1, s) == 1
+    assert lib.fcqt_analysis_static(tab, p, None, p, p, 0, 1, s) == 1
+    assert lib.fcqt_analysis_static(tab, p, p, p, p, 0, 0, s) == 1
+    assert lib.fcqt_analysis_static(tab, p, ctypes.c_void_p(4100), p, p, 0, 1, s) == 2
+    bad = ctypes.byref(Tables(tw_pass=16, tw_half=16, tw_stage=16, tasks=16, ntasks=68, ncoef=10, coef_span=132992))
+    assert lib.fcqt_analysis_static(bad, p, p, p, p, 0, 1, s) == 1
+
+
 def test_package_descriptor_declares_the_task_coverage(factored_tables):
     """The table builder's coef_span is the task table's coverage, equal to
     ncoef for the [3,4,2]/[8,16,32] layout."""
