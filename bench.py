@@ -576,6 +576,15 @@ def main():
                         "roundtrip_snr_db_min_row": rt_rows, "coef_snr_db_vs_torch_fft": coef_db,
                         "replay_vs_eager_db": rep_db,
                         "input": "configs[1] sinusoids+noise" if B == 1 else "randn N(0,1) seed 0"}
+        # the single-launch directions (one cooperative launch each, the
+        # reference's persistent pair), stream-launched back to back
+        pstep = lambda x=x: f.persist_inv(*f.persist_fwd(x))
+        with torch.no_grad():
+            same = bool(torch.equal(pstep(), eager))
+            pms = min(per_step_ms(pstep), per_step_ms(pstep))
+        per_batch[B]["single_launch"] = {"ms": pms, "round_trips_per_s": B / (pms * 1e-3),
+                                         "equal_to_six_launch_bitwise": same, "launch_mode": "stream launches",
+                                         "launches_per_round_trip": 2}
         if not args.no_lib_baseline:
             bms, bmode, bout = torch_fft_baseline(cqt_gpu, x)
             per_batch[B].update({"hipfft_baseline_ms": bms, "hipfft_baseline_mode": bmode,
@@ -583,8 +592,21 @@ def main():
                                  "hipfft_baseline_roundtrip_snr_db": snr_db(x, bout)})
         log(f"B={B}: {ms:.4f} ms ({mode})  {per_batch[B]['round_trips_per_s']:.0f} rt/s  "
             f"{per_batch[B]['hbm_gbps']:.0f} GB/s  rt {rt_rows:.1f} dB  coef {coef_db:.1f} dB"
+            f"  single-launch {pms:.4f} ms (equal: {same})"
             + (f"  hipFFT {per_batch[B]['hipfft_baseline_ms']:.4f} ms ({per_batch[B]['hipfft_baseline_mode']})"
                if not args.no_lib_baseline else ""))
+
+    # the per-launch floor on this runtime: the library's smallest kernel (a
+    # fill of four floats) stream-launched back to back; a round trip is six
+    # launches, so at batch 1 it cannot take less than about six of these
+    from flash_cqt import _native
+    tiny = torch.zeros(4, device=dev)
+    sh = _native.stream_handle(dev.index)
+    floor_ms = min(per_step_ms(lambda: f.lib.fcqt_fill_zero(tiny.data_ptr(), 4, sh), steps=200)
+                   for _ in range(3))
+    per_batch[1]["launch_floor"] = {"ms_per_launch": floor_ms, "launches_per_round_trip": 6,
+                                    "kernel": "k_fill_zero of 4 floats, stream-launched back to back"}
+    log(f"launch floor: {floor_ms * 1e3:.2f} us per kernel launch (6 per round trip)")
 
     # ---- the timed region: exactly K steps of the batch, in the faster launch mode
     B = args.batch

@@ -22,7 +22,7 @@ import sys
 ROOT = pathlib.Path(__file__).resolve().parent
 CSRC = ROOT / "csrc"
 OUT = ROOT / "flash_cqt" / "_lib" / "libflashcqt.so"
-SOURCES = ("abi.hip", "bands.hip", "packed_fft.hip", "image.hip")
+SOURCES = ("abi.hip", "bands.hip", "packed_fft.hip", "image.hip", "persist.hip")
 ARCH = "gfx950"
 
 

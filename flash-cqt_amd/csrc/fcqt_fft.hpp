@@ -375,7 +375,7 @@ __device__ __forceinline__ void fft_unit(float2* v, float2* s, int t, const floa
 // Spread consecutive workgroup ids over the 8 XCDs' L2s so that each XCD
 // receives a contiguous range of logical ids (the hardware dispatches ids
 // round-robin over XCDs). Bijective on [0, G).
-__device__ __forceinline__ int xcd_remap(int lin, int G) {
+__host__ __device__ __forceinline__ int xcd_remap(int lin, int G) {
     const int q = G >> 3, rem = G & 7;
     const int xcd = lin & 7, idx = lin >> 3;
     return xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
@@ -384,7 +384,7 @@ __device__ __forceinline__ int xcd_remap(int lin, int G) {
 // The same per-XCD ranges walked from their ends: a kernel that reads what
 // the previous kernel of the same grid wrote starts with that kernel's
 // last (most recently written, still cached) workgroups. Bijective on [0, G).
-__device__ __forceinline__ int xcd_remap_reverse(int lin, int G) {
+__host__ __device__ __forceinline__ int xcd_remap_reverse(int lin, int G) {
     const int q = G >> 3, rem = G & 7;
     const int xcd = lin & 7, idx = lin >> 3;
     const int n = xcd < rem ? q + 1 : q;

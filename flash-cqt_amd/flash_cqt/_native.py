@@ -22,7 +22,7 @@ EXPORTS = ("fcqt_abi_version", "fcqt_status_string", "fcqt_last_hip_error",
            "fcqt_packed_fft_inv", "fcqt_analysis", "fcqt_synthesis", "fcqt_fill_zero",
            "fcqt_slice_fft_fwd", "fcqt_route_bands_sliced", "fcqt_scatter_bands_sliced",
            "fcqt_overlap_add", "fcqt_stream_overlap", "fcqt_image_check", "fcqt_tables_upload",
-           "fcqt_workspace_sizes", "fcqt_analysis_static")
+           "fcqt_workspace_sizes", "fcqt_analysis_static", "fcqt_persist_analysis", "fcqt_persist_synthesis")
 
 
 class Tables(ctypes.Structure):
@@ -91,6 +91,8 @@ def load():
         "fcqt_tables_upload": ([ctypes.c_char_p, I64, P, I64, S, ctypes.POINTER(EngineTables)], ctypes.c_int),
         "fcqt_workspace_sizes": ([T, I64, ctypes.POINTER(Sizes)], ctypes.c_int),
         "fcqt_analysis_static": ([T, P, P, P, P, ctypes.c_int, I64, S], ctypes.c_int),
+        "fcqt_persist_analysis": ([T, P, P, P, P, ctypes.c_int, P, P, I64, S], ctypes.c_int),
+        "fcqt_persist_synthesis": ([T, P, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -308,14 +308,40 @@ class FusedOctCQT:
     # --------------------------------------- reference entry points kept
 
     def persist_fwd(self, x):
-        """The reference's single-launch forward (fused.py:748-762). On MI355X
-        a cooperative launch alone costs more than this engine's three
-        forward kernels, so this runs fwd; same outputs (workspace views)."""
-        return self.fwd(x)
+        """The reference's single-launch forward (fused.py:748-762,
+        persist2.cu:140-175): the whole analysis as one cooperative launch
+        (fcqt_persist_analysis: column tiles, grid barrier, row tiles, grid
+        barrier, band tasks). Same outputs as fwd, bit for bit (workspace
+        views). Not for graph capture."""
+        self._check_x(x)
+        B = x.shape[0]
+        w = self._workspace(B)
+        p = self._wp[B]
+        _native.check(self.lib.fcqt_persist_analysis(self._ct, self._tp["route"], x.data_ptr(), p["KR"], p["KI"],
+                                                     _native.PLANAR, p["X"], p["W"], B,
+                                                     _native.stream_handle(self.dev.index)), "persist_analysis")
+        return w["KR"], w["KI"]
 
     def persist_inv(self, KR, KI):
-        """The reference's single-launch inverse (fused.py:764-778); runs bwd."""
-        return self.bwd(KR, KI)
+        """The reference's single-launch inverse (fused.py:764-778,
+        persist2.cu:177-222): the whole synthesis as one cooperative launch
+        (fcqt_persist_synthesis: band scatter, grid barrier, inverse column
+        tiles, grid barrier, inverse row tiles). Same output as bwd, bit for
+        bit (a workspace view). Not for graph capture."""
+        B = KR.shape[0] if KR.dim() else 0
+        if B < 1 or KR.shape != (B, self.ncoef) or KI.shape != (B, self.ncoef):
+            raise ValueError(f"KR, KI must be [B, {self.ncoef}]")
+        _native.require_device(KR, "KR")
+        _native.require_device(KI, "KI")
+        if KR.device != self.dev or KI.device != self.dev:
+            raise ValueError(f"KR, KI must be on {self.dev}")
+        w = self._workspace(B)
+        p = self._wp[B]
+        _native.check(self.lib.fcqt_persist_synthesis(self._ct, self._tp["scat"], self._tp["ovf_scat"],
+                                                      KR.data_ptr(), KI.data_ptr(), _native.PLANAR, p["F"], p["W"],
+                                                      p["XO"], B, _native.stream_handle(self.dev.index)),
+                      "persist_synthesis")
+        return w["XO"]
 
     def bench_parts(self, x, reps=50):
         """Median ms per engine part for input x [B, 65536], each part

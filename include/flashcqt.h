@@ -225,6 +225,21 @@ int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                   float* coef_re, float* coef_im, int layout,
                   float* xs, float* work, int64_t batch, hipStream_t stream);
 
+/* Single-launch directions: the same transforms as fcqt_analysis and
+ * fcqt_synthesis (same arguments and buffer rules, same results bit for
+ * bit), each run as ONE cooperative launch (hipLaunchCooperativeKernel) of
+ * workgroups resident for the whole direction, with grid-wide barriers
+ * where fcqt_analysis / fcqt_synthesis have kernel boundaries. Not for
+ * hipGraph capture. FCQT_ELAUNCH if the runtime refuses the cooperative
+ * launch. Replace the reference's fwd2 / inv2 (persist2.cu:140-222, reached
+ * through FusedOctCQT.persist_fwd / persist_inv, fused.py:748-778). */
+int fcqt_persist_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
+                          float* coef_re, float* coef_im, int layout,
+                          float* xs, float* work, int64_t batch, hipStream_t stream);
+int fcqt_persist_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* ovf,
+                           const float* coef_re, const float* coef_im, int layout,
+                           float* f, float* work, float* y, int64_t batch, hipStream_t stream);
+
 /* Allocation-free analysis: fcqt_analysis with the spectrum X and the work
  * buffer taken from a static device array of the library (each GPU holds its
  * own copy, FCQT_STATIC_MAX_BATCH slices = 8.4 MB, until the process ends),

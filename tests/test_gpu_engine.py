@@ -645,6 +645,37 @@ def test_reference_entry_points(fused):
     assert [p[0] for p in parts][1] == "fwd route + band idft" and all(p[1] > 0 for p in parts)
 
 
+@pytest.mark.parametrize("B", [1, 5, 64, 130])
+def test_single_launch_directions_equal_six_launch_bitwise(fused, B):
+    """fcqt_persist_analysis / fcqt_persist_synthesis (one cooperative launch
+    per direction, grid barriers between the phases) against the six-launch
+    path, bit for bit; B = 130 has more tiles than resident workgroups, so
+    the phases' grid-stride loops run several tiles per workgroup."""
+    from flash_cqt import _native
+    print(f"single-launch directions: batch {B}", flush=True)
+    rs = np.random.RandomState(900 + B)
+    x = gpu(rs.standard_normal((B, N)).astype(np.float32))
+    KR, KI = fused.fwd(x)
+    k = torch.complex(KR, KI).clone()
+    y = fused.bwd(KR, KI).clone()
+    PR, PI = fused.persist_fwd(x)
+    assert torch.equal(torch.complex(PR, PI), k)
+    assert torch.equal(fused.persist_inv(PR, PI), y)
+    if B == 5:   # the interleaved layout through the C ABI
+        kc = torch.empty(B, fused.ncoef, dtype=torch.complex64, device=_dev())
+        w = fused._workspace(B)
+        _native.check(fused.lib.fcqt_persist_analysis(fused._ct, fused._tp["route"], x.data_ptr(), kc.data_ptr(),
+                                                      None, _native.INTERLEAVED, w["X"].data_ptr(),
+                                                      w["W"].data_ptr(), B, _native.stream_handle(0)), "persist")
+        yi = torch.empty(B, N, device=_dev())
+        _native.check(fused.lib.fcqt_persist_synthesis(fused._ct, fused._tp["scat"], fused._tp["ovf_scat"],
+                                                       kc.data_ptr(), None, _native.INTERLEAVED, w["F"].data_ptr(),
+                                                       w["W"].data_ptr(), yi.data_ptr(), B,
+                                                       _native.stream_handle(0)), "persist")
+        torch.cuda.synchronize()
+        assert torch.equal(kc, k) and torch.equal(yi, y)
+
+
 # ------------------------------------------------------------- errors
 
 def test_bad_inputs_rejected(fused):

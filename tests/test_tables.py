@@ -335,7 +335,7 @@ def test_narrow_pass_shapes_equal_wide_cpu(factored_tables):
 
 def test_narrow_shape_constants_match_kernels_cpu():
     """The simulator's tile shapes and batch threshold are the kernels'."""
-    src = (ROOT / "flash-cqt_amd" / "csrc" / "packed_fft.hip").read_text()
+    src = (ROOT / "flash-cqt_amd" / "csrc" / "fcqt_passes.hpp").read_text()
     import re
     def const(name):
         return int(re.search(rf"\b{name}\s*=\s*(\d+)", src).group(1))
@@ -358,3 +358,29 @@ def test_xcd_remaps_are_bijections_with_shared_ranges_cpu():
             b = [rev[l] for l in range(x, G, 8)]
             assert a == sorted(a) and b == sorted(b, reverse=True) and sorted(a) == sorted(b)
             assert not a or a == list(range(a[0], a[0] + len(a)))
+
+
+def test_xcd_map_replicas_equal_the_kernels_maps_cpu(tmp_path):
+    """The simulator's xcd_remap / xcd_remap_reverse replicas against the
+    kernels' own functions, compiled for the host from fcqt_fft.hpp (no GPU
+    needed), on grid sizes of every residue mod 8 and the engine's grids."""
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not pathlib.Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    exe = tmp_path / "xcd_maps"
+    r = subprocess.run([hipcc, "-O1", "-std=c++17", "--offload-arch=gfx950", str(ROOT / "tests" / "c" / "xcd_maps.hip"),
+                        "-o", str(exe)], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    grids = [1, 2, 7, 8, 9, 13, 68, 130, 1088, 4352]
+    out = subprocess.run([str(exe)] + [str(g) for g in grids], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    lines = out.stdout.strip().splitlines()
+    assert len(lines) == len(grids)
+    for G, ln in zip(grids, lines):
+        head, rev = ln.split("|")
+        vals = [int(v) for v in head.split()]
+        assert vals[0] == G
+        assert vals[1:] == [ks.xcd_remap(l, G) for l in range(G)]
+        assert [int(v) for v in rev.split()] == [ks.xcd_remap_reverse(l, G) for l in range(G)]
