@@ -349,6 +349,51 @@ def _cpu_baseline(port, cores, batch, budget_s, budget_b1_s, max_reps):
             "per_batch": per_batch}
 
 
+# ---------------------------------------------------- single-launch path
+
+def single_launch(f, x, eager):
+    """The single-launch directions (one cooperative launch each, the
+    reference's persistent pair) at the batch of x, stream-launched back to
+    back, and whether they reproduce the six-launch round trip bit for bit."""
+    step = lambda: f.persist_inv(*f.persist_fwd(x))
+    with torch.no_grad():
+        same = bool(torch.equal(step(), eager))
+        ms = min(per_step_ms(step), per_step_ms(step))
+    return {"ms": ms, "round_trips_per_s": x.shape[0] / (ms * 1e-3), "equal_to_six_launch_bitwise": same,
+            "launch_mode": "stream launches", "launches_per_round_trip": 2}
+
+
+def launch_floor(f, dev):
+    """The per-launch floor on this runtime: the library's smallest kernel (a
+    fill of four floats) stream-launched back to back. A round trip is six
+    launches, so at batch 1 it takes at least about six of these."""
+    from flash_cqt import _native
+    tiny = torch.zeros(4, device=dev)
+    sh = _native.stream_handle(dev.index)
+    ms = min(per_step_ms(lambda: f.lib.fcqt_fill_zero(tiny.data_ptr(), 4, sh), steps=200) for _ in range(3))
+    log(f"launch floor: {ms * 1e3:.2f} us per kernel launch (6 per round trip)")
+    return {"ms_per_launch": ms, "launches_per_round_trip": 6,
+            "kernel": "k_fill_zero of 4 floats, stream-launched back to back"}
+
+
+def single_launch_workload(f, dev):
+    """--single-launch-only: both paths at batches 1, 16, 64 and the
+    per-launch floor, for a kernel trace of the cooperative kernels."""
+    out = {"launch_floor": launch_floor(f, dev), "per_batch": {}}
+    for B in (1, 16, 64):
+        x = (torch.from_numpy(sinusoids()) if B == 1 else randn(B, 0)).to(dev)
+        fn = lambda x=x: f.bwd(*f.fwd(x))
+        with torch.no_grad():
+            eager = fn().clone()
+        six = min(per_step_ms(fn), per_step_ms(fn))
+        r = single_launch(f, x, eager)
+        r["six_launch_ms"] = six
+        out["per_batch"][str(B)] = r
+        log(f"B={B}: six launches {six:.4f} ms, single launch per direction {r['ms']:.4f} ms "
+            f"(bitwise equal: {r['equal_to_six_launch_bitwise']})")
+    return out
+
+
 # ------------------------------------------------------------ peak memory
 
 def peak_mb(fn):
@@ -526,6 +571,10 @@ def main():
     ap.add_argument("--no-lib-baseline", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--sliced-only", action="store_true")
+    ap.add_argument("--no-single-launch", action="store_true",
+                    help="skip the single-launch (cooperative) directions")
+    ap.add_argument("--single-launch-only", action="store_true",
+                    help="time only the single-launch directions and the per-launch floor; print their JSON")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -547,6 +596,9 @@ def main():
         return
     cqt_gpu = OctCQT([3, 4, 2], [8, 16, 32], fs=FS, audio_len=N, device=dev)
     f = FusedOctCQT(cqt_gpu, dev)
+    if args.single_launch_only:
+        print(json.dumps(json_safe(single_launch_workload(f, dev))), flush=True)
+        return
     if args.kernels_only:
         kernels_only(f, args.batch, max(1, args.kernel_reps // 4))
         return
@@ -576,15 +628,8 @@ def main():
                         "roundtrip_snr_db_min_row": rt_rows, "coef_snr_db_vs_torch_fft": coef_db,
                         "replay_vs_eager_db": rep_db,
                         "input": "configs[1] sinusoids+noise" if B == 1 else "randn N(0,1) seed 0"}
-        # the single-launch directions (one cooperative launch each, the
-        # reference's persistent pair), stream-launched back to back
-        pstep = lambda x=x: f.persist_inv(*f.persist_fwd(x))
-        with torch.no_grad():
-            same = bool(torch.equal(pstep(), eager))
-            pms = min(per_step_ms(pstep), per_step_ms(pstep))
-        per_batch[B]["single_launch"] = {"ms": pms, "round_trips_per_s": B / (pms * 1e-3),
-                                         "equal_to_six_launch_bitwise": same, "launch_mode": "stream launches",
-                                         "launches_per_round_trip": 2}
+        if not args.no_single_launch:
+            per_batch[B]["single_launch"] = single_launch(f, x, eager)
         if not args.no_lib_baseline:
             bms, bmode, bout = torch_fft_baseline(cqt_gpu, x)
             per_batch[B].update({"hipfft_baseline_ms": bms, "hipfft_baseline_mode": bmode,
@@ -592,21 +637,12 @@ def main():
                                  "hipfft_baseline_roundtrip_snr_db": snr_db(x, bout)})
         log(f"B={B}: {ms:.4f} ms ({mode})  {per_batch[B]['round_trips_per_s']:.0f} rt/s  "
             f"{per_batch[B]['hbm_gbps']:.0f} GB/s  rt {rt_rows:.1f} dB  coef {coef_db:.1f} dB"
-            f"  single-launch {pms:.4f} ms (equal: {same})"
+            + (f"  single-launch {per_batch[B]['single_launch']['ms']:.4f} ms"
+               if "single_launch" in per_batch[B] else "")
             + (f"  hipFFT {per_batch[B]['hipfft_baseline_ms']:.4f} ms ({per_batch[B]['hipfft_baseline_mode']})"
                if not args.no_lib_baseline else ""))
 
-    # the per-launch floor on this runtime: the library's smallest kernel (a
-    # fill of four floats) stream-launched back to back; a round trip is six
-    # launches, so at batch 1 it cannot take less than about six of these
-    from flash_cqt import _native
-    tiny = torch.zeros(4, device=dev)
-    sh = _native.stream_handle(dev.index)
-    floor_ms = min(per_step_ms(lambda: f.lib.fcqt_fill_zero(tiny.data_ptr(), 4, sh), steps=200)
-                   for _ in range(3))
-    per_batch[1]["launch_floor"] = {"ms_per_launch": floor_ms, "launches_per_round_trip": 6,
-                                    "kernel": "k_fill_zero of 4 floats, stream-launched back to back"}
-    log(f"launch floor: {floor_ms * 1e3:.2f} us per kernel launch (6 per round trip)")
+    per_batch[1]["launch_floor"] = launch_floor(f, dev)
 
     # ---- the timed region: exactly K steps of the batch, in the faster launch mode
     B = args.batch
