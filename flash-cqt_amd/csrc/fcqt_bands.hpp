@@ -93,14 +93,15 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
     fetch_tw2<M, kBandThreads>(c2, tws, threadIdx.x);
     Tw3<M> w3;
     load_tw3<M>(w3, tws, t);
-    // v = w X[k], conjugated for taps past Nyquist
+    // v = w X[k], conjugated for taps past Nyquist: the record's weight
+    // carries the conjugation in its sign bit (weights are >= 0), so
+    // v = (|w| Re X, w Im X)
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const float2 x = xb[min((unsigned)rv[r].x & 0x7fffffffu, (unsigned)kL)];
+        const float2 x = xb[min((unsigned)rv[r].x, (unsigned)kL)];
         const float w = __int_as_float(rv[r].y);
-        const float im = __int_as_float(__float_as_int(w * x.y) ^ (rv[r].x & (int)0x80000000));
-        v[r] = make_float2(w * x.x, im);
+        v[r] = make_float2(fabsf(w) * x.x, w * x.y);
     }
     put_tw2<M, kBandThreads>(tw2, c2, threadIdx.x);
     fft_unit<M, +1>(v, lds + u * P::US, t, tw2, w3);

@@ -86,11 +86,11 @@ int parse(const void* image, int64_t len, SecRef* secs, fcqt_image_info* info) {
         if (end > ncoef) return FCQT_EARG;
         span = end > span ? end : span;
     }
-    // route records {bin | conj << 31, weight}: bins inside the spectrum
+    // route records {bin, signed weight}: bins inside the spectrum
     for (uint32_t id : {kSecRoute, kSecRouteB}) {
         if (!shape(id, 4, (uint64_t)ntasks * kRecordsPerTask * 2)) return FCQT_EARG;
         for (uint64_t r = 0; r < (uint64_t)ntasks * kRecordsPerTask; ++r)
-            if (((uint32_t)i32(secs[id], 2 * r) & 0x7fffffffu) > (uint32_t)kL) return FCQT_EARG;
+            if ((uint32_t)i32(secs[id], 2 * r) > (uint32_t)kL) return FCQT_EARG;
     }
     // scatter records {slot | mode << 30, gain}: slots inside an F row, modes 0..2
     for (uint32_t id : {kSecScat, kSecScatA}) {

@@ -2,9 +2,11 @@
 
 Everything the kernels need that does not depend on the batch:
   route    analysis route records in the band kernels' order
-           [task][slot][thread] (kernel_taps): {bin | conj << 31, weight
-           bits}, the tap's gather bin and fp32 weight window / M
-           (route_taps: the weights in natural tap order). The kernel gathers
+           [task][slot][thread] (kernel_taps): {bin, signed weight bits},
+           the tap's gather bin and fp32 weight window / M (route_taps: the
+           weights in natural tap order), negated for the taps that read
+           the conjugate (the weights are >= 0, so the sign bit carries the
+           conjugation: the kernel takes |w| Re X and w Im X). The kernel gathers
            the real FFT X (computed by the forward passes, untangle included)
            at the tap's bin, conjugated for taps past nn/2 (DC/Nyquist bands),
            multiplies by the weight and runs the band's unscaled inverse DFT.
@@ -232,8 +234,9 @@ def build(groups, nn=N, noct=None):
     check_tasks(tasks, ncoef, bands)
     check_band_taps(bands, groups)
     tin, tout = kernel_taps(tasks), kernel_taps(tasks, out=True)
-    kbin = (k | (cf.astype(np.int64) << 31)).astype(np.uint32).view(np.int32)
-    route_rec = lambda w: _kernel_order(np.stack([kbin, _bits(w)], axis=1), tin)
+    assert not np.any(np.signbit(route)) and not np.any(np.signbit(route_b)), "route weights must be >= 0"
+    kbin = k.astype(np.int32)
+    route_rec = lambda w: _kernel_order(np.stack([kbin, _bits(np.where(cf, -w, w))], axis=1), tin)
     return dict(route=route_rec(route), route_b=route_rec(route_b), route_taps=route, route_b_taps=route_b,
                 scat=_kernel_order(scat, tout), scat_a=_kernel_order(scat_a, tout),
                 scat_taps=scat, scat_a_taps=scat_a, tasks=tasks, bands=bands,

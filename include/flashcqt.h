@@ -174,9 +174,10 @@ int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* xs, float
  * Windowed band gathers + band inverse DFTs: coefficient m of band b is
  *   C_b[m] = sum_j w_j X~[k_j] e^{+2 pi i jm/M_b}
  * where X~ is X, or its conjugate for taps past N/2 (folded to N - k). One
- * record per tap {k | conj << 31, fp32 weight bits}: window/M gives the
- * analysis, dual window * 2/N (halved at bins 0 and L) the synthesis
- * adjoint; taps outside the window have weight 0.
+ * record per tap {k, fp32 weight bits}: window/M gives the analysis, dual
+ * window * 2/N (halved at bins 0 and L) the synthesis adjoint; taps outside
+ * the window have weight 0. The weights are >= 0, and a tap that reads the
+ * conjugate stores its weight negated: the kernel forms (|w| Re X, w Im X).
  *   xs      [batch][FCQT_XSTRIDE] complex real-FFT spectrum (fcqt_packed_fft_fwd)
  *   coef    layout FCQT_PLANAR: coef_re, coef_im [batch][ncoef] fp32
  *           layout FCQT_INTERLEAVED: coef_re is [batch][ncoef] complex, coef_im unused

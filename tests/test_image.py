@@ -92,6 +92,7 @@ def test_corrupted_images_are_refused(lib, image, factored_tables):
     bad["negative first"] = _patched(image, 4, 1, -5)
     bad["ncoef below coverage"] = _patched(image, 12, 0, int(t["ncoef"]) - 1, np.int64)
     bad["route bin"] = _patched(image, 5, 2 * 777, 32769)
+    bad["route bin with a high bit"] = _patched(image, 5, 2 * 778, np.int32(np.uint32(5 | (1 << 31)).view(np.int32)))
     bad["adjoint route bin"] = _patched(image, 6, 2 * 1234, 40000)
     bad["scatter slot"] = _patched(image, 7, 2 * 99, 2 * 32832 + 2 * 1024)
     bad["scatter mode"] = _patched(image, 8, 2 * 5, np.int32(np.uint32(3 << 30).view(np.int32)))

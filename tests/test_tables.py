@@ -73,10 +73,11 @@ def test_weights_and_band_descriptors(factored_tables, pkg_cqt_cpu):
     for name in ("route", "route_b"):
         rec = t[name].reshape(tin.shape + (2,))
         live = tin >= 0
-        word = rec[..., 0].view(np.uint32)
-        assert np.array_equal((word & 0x7FFFFFFF)[live], k[tin[live]])
-        assert np.array_equal((word >> 31)[live].astype(bool), cf[tin[live]])
-        assert np.array_equal(rec[..., 1].view(np.float32)[live], t[name + "_taps"][tin[live]])
+        word = rec[..., 0]
+        w = rec[..., 1].view(np.float32)
+        assert np.array_equal(word[live], k[tin[live]])
+        assert np.array_equal(np.signbit(w)[live], cf[tin[live]])            # conjugation in the sign bit
+        assert np.array_equal(np.abs(w)[live], t[name + "_taps"][tin[live]])
         assert not np.any(rec[~live])
     for name in ("scat", "scat_a"):
         rec = t[name].reshape(tout.shape + (2,))
