@@ -16,11 +16,12 @@
 // load of a wave is one contiguous 512-byte run.
 //
 // Analysis prologue (slot r of a thread = tap t + T r of its band):
-// v = w X[k], conjugated for taps past Nyquist, from the record
-// {k | conj << 31, w}: X is the real FFT of the slice (the forward row pass
-// already untangled the packed spectrum) and w one fp32 weight per tap
-// (window / M for the analysis, dual window * 2/N for the synthesis
-// adjoint); taps outside the window carry w = 0.
+// v = w X[k], conjugated for taps past Nyquist, from the record {k, ±w}:
+// X is the real FFT of the slice (the forward row pass already untangled
+// the packed spectrum) and w one fp32 weight per tap (window / M for the
+// analysis, dual window * 2/N for the synthesis adjoint), stored negated
+// for a tap that reads the conjugate (weights are >= 0); taps outside the
+// window carry w = 0.
 // Synthesis epilogue (slot q RL + r = output t + T q + r OS): the tap stores
 // (gr Re D, gi Im D) to its own slot of the half-spectrum buffer F, from the
 // record {slot | mode << 30, gr} (plane P0 or P1 at the tap's bin, or an
