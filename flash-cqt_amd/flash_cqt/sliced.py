@@ -205,20 +205,27 @@ class SlicedCQT:
         uses its leading rows. Rows are independent, and F is only ever used
         with the synthesis scatter table, so the slots that table never
         writes stay zero in every row (F is zeroed when allocated). Memory is
-        therefore bounded by the largest call, whatever the signal lengths."""
+        therefore bounded by the largest call, whatever the signal lengths.
+
+        A set that served a call under stream capture (hipGraph) stays
+        allocated after a larger set replaces it: the recorded launches hold
+        its addresses and write into it on every replay."""
         cache, ptrs = self._caches(f)
         B = nsig * S
         full = cache.get("rows")
         if full is None or full["B"] < B:
             from . import tables as T
             dev = f.dev
-            cache.clear()
+            if full is not None and full["captured"]:
+                cache.setdefault("recorded", []).append(full)
             ptrs.clear()                 # cached raw pointers refer to the old buffers
-            cache["rows"] = full = dict(B=B, X=torch.empty(B, T.XSTRIDE, 2, device=dev),
+            cache["rows"] = full = dict(B=B, captured=False, X=torch.empty(B, T.XSTRIDE, 2, device=dev),
                                         W=torch.empty(B, T.L, 2, device=dev),
                                         F=torch.zeros(B, T.FROW, 2, device=dev),
                                         Y=torch.empty(B, self.sl_len, device=dev))
-        return {k: v[:B] for k, v in full.items() if k != "B"}
+        if torch.cuda.is_current_stream_capturing():
+            full["captured"] = True
+        return {k: full[k][:B] for k in ("X", "W", "F", "Y")}
 
     def _tw32(self):
         tw = self.__dict__.get("_tw32_cache")
@@ -324,12 +331,14 @@ class SlicedCQT:
     def _stream_ptrs(self, f, nsig):
         """Raw pointers of the one-slice buffers for nsig signals (the engine's
         own, sized at allocation), so a streamed step is two C-ABI calls."""
-        cache = self._caches(f)[1]
+        bufs, cache = self._caches(f)
         st = cache.get(nsig)
         if st is None:
             st = {k: v.data_ptr() for k, v in self._ws(f, nsig, 1).items()}
             st["tw"] = self._tw32().data_ptr()
             cache[nsig] = st
+        elif torch.cuda.is_current_stream_capturing():
+            bufs["rows"]["captured"] = True      # recorded launches keep these addresses
         return st
 
     def _stream_slice_fused(self, f, prev, chunk, k):

@@ -556,6 +556,30 @@ def test_sliced_engine_swap_rebuilds_buffers():
     assert s._cache_owner is s.cqt.f
 
 
+def test_sliced_graph_replays_after_buffer_growth():
+    """A graph recorded over SlicedCQT round trips keeps giving the eager
+    result after a longer signal grows the engine's buffers: the recorded
+    buffer set stays allocated. Eager calls run between the replays."""
+    from flash_cqt import Graphed, SlicedCQT
+    s = SlicedCQT(device=_dev())
+    xs = gpu(np.random.RandomState(21).standard_normal((1, 1, 2 * s.hop)))
+    xl = gpu(np.random.RandomState(22).standard_normal((2, 1, 9 * s.hop)))
+    with torch.no_grad():
+        ref = s.bwd(*s.fwd(xs), length=xs.shape[-1]).clone()
+        g = Graphed(lambda a: s.bwd(*s.fwd(a), length=a.shape[-1]), xs)
+        recorded = s._fused_ws["rows"]
+        assert recorded["captured"]
+        yl = s.bwd(*s.fwd(xl), length=xl.shape[-1])      # grows the buffer set
+        assert s._fused_ws["rows"] is not recorded and recorded in s._fused_ws["recorded"]
+        assert snr_db(cnp(xl), cnp(yl)) > 125
+        for _ in range(3):
+            y = g(xs)
+            torch.cuda.synchronize()
+            assert torch.equal(y, ref)
+            s.bwd(*s.fwd(xl), length=xl.shape[-1])
+            torch.cuda.synchronize()
+
+
 def test_sliced_fused_framing_equals_engine_composition():
     """The fused framing (slices read from the signal, block-layout stores,
     overlap-add kernel) is bitwise the engine + torch-glue composition that

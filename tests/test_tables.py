@@ -251,6 +251,42 @@ def test_sliced_block_buffer_detection_cpu():
     assert torch.equal(noside[:tail], coef[:tail]) and not noside[tail:].any()
 
 
+def test_sliced_buffer_sets_kept_for_recorded_graphs_cpu(monkeypatch):
+    """SlicedCQT's engine buffers: one set, grown to the largest call, smaller
+    calls get leading rows. A set that served a call under stream capture is
+    kept allocated when a larger set replaces it (recorded launches hold its
+    addresses); an unrecorded set is dropped."""
+    import types
+    from flash_cqt import tables as T
+    from flash_cqt.sliced import SlicedCQT
+    s = SlicedCQT.__new__(SlicedCQT)                     # host logic only
+    s.sl_len = T.N
+    f = types.SimpleNamespace(dev=torch.device("cpu"))
+    capturing = [False]
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: capturing[0])
+    w = s._ws(f, 1, 2)
+    assert w["X"].shape == (2, T.XSTRIDE, 2) and w["F"].shape == (2, T.FROW, 2) and not w["F"].any()
+    first = s._fused_ws["rows"]
+    s._ws(f, 1, 3)                                       # grows; the first set was never recorded
+    assert s._fused_ws["rows"] is not first and "recorded" not in s._fused_ws
+    second = s._fused_ws["rows"]
+    assert s._ws(f, 1, 2)["W"].data_ptr() == second["W"].data_ptr()      # leading rows
+    capturing[0] = True
+    s._ws(f, 1, 2)                                       # served under capture: marked
+    capturing[0] = False
+    third_call = s._ws(f, 2, 2)                          # grows again
+    assert s._fused_ws["recorded"] == [second] and s._fused_ws["rows"]["B"] == 4
+    assert third_call["Y"].shape == (4, T.N)
+    # the streamed path marks the set it hands out cached pointers for
+    s._stream_ptrs = SlicedCQT._stream_ptrs.__get__(s)
+    s._tw32 = lambda: torch.zeros(1)
+    s._stream_ptrs(f, 1)
+    capturing[0] = True
+    s._stream_ptrs(f, 1)
+    capturing[0] = False
+    assert s._fused_ws["rows"]["captured"]
+
+
 def test_product_sliced_host_framing_matches_reference_cpu(golden):
     """flash_cqt.SlicedCQT with the torch engine on the CPU (the host framing
     that autograd and the torch engine use) against the reference's own
