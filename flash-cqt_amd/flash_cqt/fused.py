@@ -42,6 +42,8 @@ def _np_groups(cqt):
 class FusedOctCQT:
     """Kernel tables, workspaces and launchers for one OctCQT at audio_len 65536."""
 
+    _PLANE_SKEW = 4096      # floats (16 KiB) between the KR and KI planes of a workspace
+
     def __init__(self, cqt, device=None):
         assert cqt.nn == N, "fused path is built for sl_len 65536"
         dev = torch.device(device) if device is not None else torch.device(cqt.device)
@@ -101,8 +103,18 @@ class FusedOctCQT:
             with torch.cuda.device(self.dev):
                 e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)
                 z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
+                # both coefficient planes in one allocation, KI starting
+                # _PLANE_SKEW floats past the end of KR: the band kernels
+                # store (load) KR[i] and KI[i] together, and with KI right at
+                # the end of a 2 MiB-aligned KR (how the caching allocator can
+                # split one freed block between two plane tensors) both
+                # streams met in the same memory channels and the route
+                # kernel ran 10-12% slower
+                n = B * self.ncoef
+                planes = z(2 * n + self._PLANE_SKEW)
                 self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=z(B, T.FROW, 2),
-                                   KR=z(B, self.ncoef), KI=z(B, self.ncoef), XO=z(B, N))
+                                   KR=planes[:n].view(B, self.ncoef),
+                                   KI=planes[n + self._PLANE_SKEW:].view(B, self.ncoef), XO=z(B, N))
             self._wp[B] = {k: v.data_ptr() for k, v in self._ws[B].items()}
         return self._ws[B]
 
