@@ -39,10 +39,21 @@ def _np_groups(cqt):
     return out
 
 
+SKEW = 4096      # floats (16 KiB): KR-to-KI plane gap, and offset of F into its allocation
+
+
+def slot_buffer(B, dev):
+    """A zeroed F buffer [B, FROW, 2] that starts SKEW floats into its
+    allocation. Large allocations start 2 MiB-aligned, and an F there
+    measured slower: the scatter's stores and the inverse column pass's
+    paired plane loads (F[bin], F[FSTRIDE + bin]) took 0.5-1.5 us longer at
+    batch 64 than with any base offset from 512 bytes on."""
+    n = B * T.FROW * 2
+    return torch.zeros(n + SKEW, dtype=torch.float32, device=dev)[SKEW:].view(B, T.FROW, 2)
+
+
 class FusedOctCQT:
     """Kernel tables, workspaces and launchers for one OctCQT at audio_len 65536."""
-
-    _PLANE_SKEW = 4096      # floats (16 KiB) between the KR and KI planes of a workspace
 
     def __init__(self, cqt, device=None):
         assert cqt.nn == N, "fused path is built for sl_len 65536"
@@ -104,17 +115,17 @@ class FusedOctCQT:
                 e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)
                 z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
                 # both coefficient planes in one allocation, KI starting
-                # _PLANE_SKEW floats past the end of KR: the band kernels
+                # SKEW floats past the end of KR: the band kernels
                 # store (load) KR[i] and KI[i] together, and with KI right at
                 # the end of a 2 MiB-aligned KR (how the caching allocator can
                 # split one freed block between two plane tensors) both
                 # streams met in the same memory channels and the route
                 # kernel ran 10-12% slower
                 n = B * self.ncoef
-                planes = z(2 * n + self._PLANE_SKEW)
-                self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=z(B, T.FROW, 2),
+                planes = z(2 * n + SKEW)
+                self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=slot_buffer(B, self.dev),
                                    KR=planes[:n].view(B, self.ncoef),
-                                   KI=planes[n + self._PLANE_SKEW:].view(B, self.ncoef), XO=z(B, N))
+                                   KI=planes[n + SKEW:].view(B, self.ncoef), XO=z(B, N))
             self._wp[B] = {k: v.data_ptr() for k, v in self._ws[B].items()}
         return self._ws[B]
 
@@ -124,7 +135,7 @@ class FusedOctCQT:
         w = self._workspace(B)
         if "FA" not in w:
             with torch.cuda.device(self.dev):
-                w["FA"] = torch.zeros(B, T.FROW, 2, dtype=torch.float32, device=self.dev)
+                w["FA"] = slot_buffer(B, self.dev)
             self._wp[B]["FA"] = w["FA"].data_ptr()
         return w["FA"]
 

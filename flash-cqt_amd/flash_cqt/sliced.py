@@ -215,13 +215,14 @@ class SlicedCQT:
         full = cache.get("rows")
         if full is None or full["B"] < B:
             from . import tables as T
+            from .fused import slot_buffer
             dev = f.dev
             if full is not None and full["captured"]:
                 cache.setdefault("recorded", []).append(full)
             ptrs.clear()                 # cached raw pointers refer to the old buffers
             cache["rows"] = full = dict(B=B, captured=False, X=torch.empty(B, T.XSTRIDE, 2, device=dev),
                                         W=torch.empty(B, T.L, 2, device=dev),
-                                        F=torch.zeros(B, T.FROW, 2, device=dev),
+                                        F=slot_buffer(B, dev),
                                         Y=torch.empty(B, self.sl_len, device=dev))
         if torch.cuda.is_current_stream_capturing():
             full["captured"] = True
