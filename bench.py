@@ -448,8 +448,7 @@ def kernel_timings(f, B, reps):
     dev = f.dev
     w = f._workspace(B)
     x = randn(B, 1).to(dev)
-    kr = torch.empty(B, f.ncoef, device=dev)
-    ki = torch.empty(B, f.ncoef, device=dev)
+    kr, ki = w["KR"], w["KI"]          # the engine's own coefficient planes (their placement matters)
     y = torch.empty(B, N, device=dev)
     # each call once through the checked wrappers (buffer sizes, devices),
     # then the same C-ABI calls with cached pointers, so that enqueueing a
@@ -513,10 +512,10 @@ def kernel_timings(f, B, reps):
     return out
 
 
-# kernel names in the profiles (the pass kernels in their wide tile shapes,
-# which batch 64 runs)
-KERNEL_SYMBOL = {"packed_fft": ("k_col_fwd<false,16>", "k_row_fwd<16>"), "route_bands": ("k_route_bands<0>",),
-                 "scatter_bands": ("k_scatter_bands<0>",), "packed_ifft": ("k_col_inv<32>", "k_row_inv<16>")}
+# kernel names in the profiles (the pass kernels in their wide tile shapes
+# and the band kernels with write-through stores, which batch 64 runs)
+KERNEL_SYMBOL = {"packed_fft": ("k_col_fwd<false,16>", "k_row_fwd<16>"), "route_bands": ("k_route_bands<0,true>",),
+                 "scatter_bands": ("k_scatter_bands<0,true>",), "packed_ifft": ("k_col_inv<32>", "k_row_inv<16>")}
 
 
 def measured_traffic(name, B):
@@ -543,8 +542,7 @@ def kernels_only(f, B, reps):
     dev = f.dev
     w = f._workspace(B)
     x = randn(B, 1).to(dev)
-    kr = torch.empty(B, f.ncoef, device=dev)
-    ki = torch.empty(B, f.ncoef, device=dev)
+    kr, ki = w["KR"], w["KI"]          # the engine's own coefficient planes (their placement matters)
     y = torch.empty(B, N, device=dev)
     src = torch.ones(16 * 1024 * 1024, device=dev)      # 64 MiB
     dst = torch.empty_like(src)

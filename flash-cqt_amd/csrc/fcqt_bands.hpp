@@ -59,13 +59,13 @@ __device__ __forceinline__ float2 load_coef(const float* __restrict__ cre, const
     else return reinterpret_cast<const float2*>(cre)[i];
 }
 
-template <int LAYOUT>
+template <int LAYOUT, bool WT>
 __device__ __forceinline__ void store_coef(float* __restrict__ cre, float* __restrict__ cim, int i, float2 v) {
     if constexpr (LAYOUT == FCQT_PLANAR) {
-        cre[i] = v.x;
-        cim[i] = v.y;
+        store_out<WT>(cre + i, v.x);
+        store_out<WT>(cim + i, v.y);
     } else {
-        reinterpret_cast<float2*>(cre)[i] = v;
+        store_out<WT>(reinterpret_cast<float2*>(cre) + i, v);
     }
 }
 
@@ -80,7 +80,7 @@ __device__ __forceinline__ void load_records(int2* rv, const int2* __restrict__ 
 // task's bands (units past the band count compute padding that is never
 // stored). The twiddle loads issue before the gathers, so their latency
 // hides under the record and gather round trips.
-template <int M, int LAYOUT>
+template <int M, int LAYOUT, bool WT>
 __device__ __forceinline__ void route_band(const int4 task, const int task_id, const int b, const int batch,
                                            const int2* rv, const float2* __restrict__ xb,
                                            float* __restrict__ cre, float* __restrict__ cim,
@@ -115,12 +115,12 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
         for (int q = 0; q < P::QL; ++q) {
 #pragma unroll
             for (int r = 0; r < P::RL; ++r)
-                store_coef<LAYOUT>(orow, oim, (t + P::T * q + r * P::OS + shift) & (M - 1), v[q * P::RL + r]);
+                store_coef<LAYOUT, WT>(orow, oim, (t + P::T * q + r * P::OS + shift) & (M - 1), v[q * P::RL + r]);
         }
     }
 }
 
-template <int M, int LAYOUT>
+template <int M, int LAYOUT, bool WT>
 __device__ __forceinline__ void scatter_band(const int4 task, const int task_id, const int b, const int batch,
                                              const int2* __restrict__ scat, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
@@ -157,7 +157,7 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
                 const unsigned mode = (unsigned)rv[i].x >> 30;
                 const unsigned slot = min((unsigned)rv[i].x & 0x3fffffffu, (unsigned)(kFRow - 1));
                 const float gi = mode == 0 ? gr : (mode == 1 ? -gr : 0.0f);
-                fb[slot] = make_float2(gr * v[i].x, gi * v[i].y);
+                store_out<WT>(fb + slot, make_float2(gr * v[i].x, gi * v[i].y));
             }
         }
     }
@@ -179,8 +179,10 @@ __device__ __forceinline__ void decode_task(int batch, int& task, int& b) {
 constexpr int kBandTaskLds = kBandLds + tw2_len<2048>();
 
 // One band task (task_id, slice b) of the route engine in caller-provided
-// LDS; the kernel below and the single-launch analysis (persist.hip) run it.
-template <int LAYOUT>
+// LDS; the band kernels and the single-launch analysis (persist.hip) run it.
+// WT: write the coefficients through the L2 (store_out), for batches whose
+// coefficient output is large.
+template <int LAYOUT, bool WT = false>
 __device__ __forceinline__ void route_task(const int task_id, const int b, const float2* __restrict__ xs,
                                            float* __restrict__ cre, float* __restrict__ cim,
                                            const int2* __restrict__ rec, const int4* __restrict__ tasks,
@@ -194,7 +196,7 @@ __device__ __forceinline__ void route_task(const int task_id, const int b, const
     const float2* xb = xs + (long)b * kXStride;
     const int4 td = tasks[task_id];
     if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
-#define FCQT_ROUTE(M_) route_band<M_, LAYOUT>(td, task_id, b, batch, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2)
+#define FCQT_ROUTE(M_) route_band<M_, LAYOUT, WT>(td, task_id, b, batch, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
         case 32: FCQT_ROUTE(32); break;
         case 64: FCQT_ROUTE(64); break;
@@ -209,8 +211,9 @@ __device__ __forceinline__ void route_task(const int task_id, const int b, const
 }
 
 
-// One band task of the scatter engine in caller-provided LDS.
-template <int LAYOUT>
+// One band task of the scatter engine in caller-provided LDS (WT: slot
+// stores through the L2, as in route_task).
+template <int LAYOUT, bool WT = false>
 __device__ __forceinline__ void scatter_task(const int task_id, const int b, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
                                              const int2* __restrict__ scat, const int4* __restrict__ tasks,
@@ -219,7 +222,7 @@ __device__ __forceinline__ void scatter_task(const int task_id, const int b, con
     float2* tw2 = lds + kBandLds;
     const int4 td = tasks[task_id];
     if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
-#define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT>(td, task_id, b, batch, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
+#define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT, WT>(td, task_id, b, batch, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
         case 32: FCQT_SCATTER(32); break;
         case 64: FCQT_SCATTER(64); break;

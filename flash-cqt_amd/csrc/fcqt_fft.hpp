@@ -49,6 +49,37 @@ __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
 __device__ __forceinline__ float2 cmulc(float2 a, float2 b) {
     return make_float2(fmaf(a.x, b.x, a.y * b.y), fmaf(a.y, b.x, -a.x * b.y));
 }
+// ------------------------------------------------------------ output stores
+// WT = true: a store that writes through this XCD's L2 (a relaxed device-scope
+// atomic store, 'sc1'), so the line goes on to the memory-side cache at once
+// instead of staying dirty in the L2 until the write-back at the end of the
+// kernel, which then no longer sits on the critical path. It pays for
+// outputs of many MB that the next kernel reads from other XCDs (or that
+// are final): the band kernels from 4 slices up and the wide inverse
+// passes. A line written this way is not kept in the writer's L2, so a
+// consumer on the same XCD no longer hits it there, and a store covering
+// half a 128-byte line costs extra bytes. The values stored are the same
+// either way.
+template <bool WT>
+__device__ __forceinline__ void store_out(float2* p, float2 v) {
+    if constexpr (WT) {
+        const unsigned long long bits =
+            ((unsigned long long)__float_as_uint(v.y) << 32) | (unsigned long long)__float_as_uint(v.x);
+        __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), bits, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *p = v;
+    }
+}
+template <bool WT>
+__device__ __forceinline__ void store_out(float* p, float v) {
+    if constexpr (WT)
+        __hip_atomic_store(reinterpret_cast<unsigned*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+
 // a * (SIGN i)   i.e. a * e^{SIGN i pi/2}
 template <int SIGN>
 __device__ __forceinline__ float2 rot4(float2 a) {

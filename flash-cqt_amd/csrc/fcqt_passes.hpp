@@ -71,7 +71,15 @@ __device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const float* 
 // Each pass is a tile body over (slice b, tile index) working in LDS the
 // caller provides (the kernels below and the single-launch kernels of
 // persist.hip run the same bodies, so both give the same bits): CPW (or RPW)
-// units, then the twiddle block.
+// units, then the twiddle block. The wide shapes (the batches above
+// kNarrowMaxBatch) of the inverse passes write their outputs through the L2
+// (store_out<true>: the inverse pair ran 1.4 us faster at batch 64). The
+// forward passes and the narrow shapes use plain stores: a write-through W
+// is no longer in the L2 when the row pass of the same slice reads it on
+// the same XCD (its hit rate fell from 0.53 to 0.06, and the round trip
+// was 0.4 us slower), and the forward row pass covers each 128-byte line of
+// X in two 64-byte halves (write-through wrote 25% more bytes). Same values
+// either way.
 template <int CPW>
 constexpr int col_lds() { return CPW * Plan<128>::US + tw2_len<128>(); }
 template <int RPW>
@@ -260,7 +268,7 @@ __device__ __forceinline__ void col_inv_tile(const int b, const int w, const flo
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) {
             const int k1 = t + 8 * q + 16 * r;
-            yb[k1 * 256 + col] = cmul(v[q * P::RL + r], tp[q * P::RL + r]);
+            store_out<CPW == kInvColsWide>(&yb[k1 * 256 + col], cmul(v[q * P::RL + r], tp[q * P::RL + r]));
         }
     }
 }
@@ -377,7 +385,7 @@ __device__ __forceinline__ void row_inv_tile(const int b, const int rg, const fl
     for (int u = 0; u < 16; ++u) {
         const int k2 = kg + 16 * u;
         const float2 w = s2[pad16(k2)];
-        yo[kk1 + 128 * k2] = make_float2(w.x * sc, -w.y * sc);
+        store_out<RPW == kRowsWide>(&yo[kk1 + 128 * k2], make_float2(w.x * sc, -w.y * sc));
     }
 }
 
