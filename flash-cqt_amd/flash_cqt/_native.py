@@ -12,7 +12,8 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
+SYNC_PER_SLICE = 64       # FCQT_SYNC_PER_SLICE: uint32 per slice in a single-launch counter buffer
 PLANAR = 0
 INTERLEAVED = 1
 
@@ -47,7 +48,7 @@ class EngineTables(ctypes.Structure):
 
 class Sizes(ctypes.Structure):
     """Mirror of struct fcqt_sizes."""
-    _fields_ = [(n, ctypes.c_int64) for n in ("signal", "spectrum", "work", "scatter", "coef_plane", "tail")]
+    _fields_ = [(n, ctypes.c_int64) for n in ("signal", "spectrum", "work", "scatter", "coef_plane", "tail", "sync")]
 
 
 class NativeError(RuntimeError):
@@ -91,8 +92,8 @@ def load():
         "fcqt_tables_upload": ([ctypes.c_char_p, I64, P, I64, S, ctypes.POINTER(EngineTables)], ctypes.c_int),
         "fcqt_workspace_sizes": ([T, I64, ctypes.POINTER(Sizes)], ctypes.c_int),
         "fcqt_analysis_static": ([T, P, P, P, P, ctypes.c_int, I64, S], ctypes.c_int),
-        "fcqt_persist_analysis": ([T, P, P, P, P, ctypes.c_int, P, P, I64, S], ctypes.c_int),
-        "fcqt_persist_synthesis": ([T, P, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_persist_analysis": ([T, P, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_persist_synthesis": ([T, P, P, P, P, ctypes.c_int, P, P, P, P, I64, S], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -139,6 +139,22 @@ class FusedOctCQT:
             self._wp[B]["FA"] = w["FA"].data_ptr()
         return w["FA"]
 
+    def sync_buffer(self, B):
+        """Stage counters of the single-launch directions for batch B
+        ((B + 1) * FCQT_SYNC_PER_SLICE uint32), zeroed on first use; every
+        call returns them to zero. The last block is the error word."""
+        w = self._workspace(B)
+        if "SYNC" not in w:
+            with torch.cuda.device(self.dev):
+                w["SYNC"] = torch.zeros((B + 1) * _native.SYNC_PER_SLICE, dtype=torch.int32, device=self.dev)
+            self._wp[B]["SYNC"] = w["SYNC"].data_ptr()
+        return w["SYNC"]
+
+    def sync_error(self, B):
+        """The single-launch error word for batch B (0: every stage wait ended
+        in time and on the right XCD). Reads device memory: synchronizes."""
+        return int(self.sync_buffer(B)[B * _native.SYNC_PER_SLICE].item())
+
     def _fbuf(self, table, B):
         return self._workspace(B)["F"] if table == "scat" else self.fa_buffer(B)
 
@@ -332,25 +348,27 @@ class FusedOctCQT:
 
     def persist_fwd(self, x):
         """The reference's single-launch forward (fused.py:748-762,
-        persist2.cu:140-175): the whole analysis as one cooperative launch
-        (fcqt_persist_analysis: column tiles, grid barrier, row tiles, grid
-        barrier, band tasks). Same outputs as fwd, bit for bit (workspace
-        views). Not for graph capture."""
+        persist2.cu:140-175): the whole analysis as one launch
+        (fcqt_persist_analysis: column tiles, row tiles and band tasks of a
+        slice on one XCD, each stage waiting for the slice's previous one).
+        Same outputs as fwd, bit for bit (workspace views)."""
         self._check_x(x)
         B = x.shape[0]
         w = self._workspace(B)
+        self.sync_buffer(B)
         p = self._wp[B]
         _native.check(self.lib.fcqt_persist_analysis(self._ct, self._tp["route"], x.data_ptr(), p["KR"], p["KI"],
-                                                     _native.PLANAR, p["X"], p["W"], B,
+                                                     _native.PLANAR, p["X"], p["W"], p["SYNC"], B,
                                                      _native.stream_handle(self.dev.index)), "persist_analysis")
         return w["KR"], w["KI"]
 
     def persist_inv(self, KR, KI):
         """The reference's single-launch inverse (fused.py:764-778,
-        persist2.cu:177-222): the whole synthesis as one cooperative launch
-        (fcqt_persist_synthesis: band scatter, grid barrier, inverse column
-        tiles, grid barrier, inverse row tiles). Same output as bwd, bit for
-        bit (a workspace view). Not for graph capture."""
+        persist2.cu:177-222): the whole synthesis as one launch
+        (fcqt_persist_synthesis: band scatter, inverse column tiles and
+        inverse row tiles of a slice on one XCD, each stage waiting for the
+        slice's previous one). Same output as bwd, bit for bit (a workspace
+        view)."""
         B = KR.shape[0] if KR.dim() else 0
         if B < 1 or KR.shape != (B, self.ncoef) or KI.shape != (B, self.ncoef):
             raise ValueError(f"KR, KI must be [B, {self.ncoef}]")
@@ -359,10 +377,11 @@ class FusedOctCQT:
         if KR.device != self.dev or KI.device != self.dev:
             raise ValueError(f"KR, KI must be on {self.dev}")
         w = self._workspace(B)
+        self.sync_buffer(B)
         p = self._wp[B]
         _native.check(self.lib.fcqt_persist_synthesis(self._ct, self._tp["scat"], self._tp["ovf_scat"],
                                                       KR.data_ptr(), KI.data_ptr(), _native.PLANAR, p["F"], p["W"],
-                                                      p["XO"], B, _native.stream_handle(self.dev.index)),
+                                                      p["XO"], p["SYNC"], B, _native.stream_handle(self.dev.index)),
                       "persist_synthesis")
         return w["XO"]
 

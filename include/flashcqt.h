@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 7
+#define FCQT_ABI_VERSION 8
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -135,6 +135,7 @@ typedef struct fcqt_sizes {
     int64_t scatter;     /* f, one per scatter table: batch * FCQT_FROW complex */
     int64_t coef_plane;  /* one FCQT_PLANAR plane: batch * ncoef fp32 (FCQT_INTERLEAVED: twice this) */
     int64_t tail;        /* fcqt_stream_overlap tail: batch (signals) * 32768 fp32 */
+    int64_t sync;        /* single-launch stage counters: (batch + 1) * FCQT_SYNC_PER_SLICE uint32 */
 } fcqt_sizes;
 
 /* Fill *out for `batch` slices (tab supplies ncoef). FCQT_EARG on a bad
@@ -227,19 +228,30 @@ int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                   float* xs, float* work, int64_t batch, hipStream_t stream);
 
 /* Single-launch directions: the same transforms as fcqt_analysis and
- * fcqt_synthesis (same arguments and buffer rules, same results bit for
- * bit), each run as ONE cooperative launch (hipLaunchCooperativeKernel) of
- * workgroups resident for the whole direction, with grid-wide barriers
- * where fcqt_analysis / fcqt_synthesis have kernel boundaries. Not for
- * hipGraph capture. FCQT_ELAUNCH if the runtime refuses the cooperative
- * launch. Replace the reference's fwd2 / inv2 (persist2.cu:140-222, reached
- * through FusedOctCQT.persist_fwd / persist_inv, fused.py:748-778). */
+ * fcqt_synthesis (same buffers and rules, same results bit for bit), each
+ * as ONE ordinary launch. Its three stages (analysis: column tiles, row
+ * tiles, band tasks; synthesis: band tasks, inverse column tiles, inverse
+ * row tiles) are workgroups of the same grid; a slice's stages all run on
+ * one XCD and each waits, through counters in `sync`, for the stage of the
+ * same slice before it, so there is no grid-wide barrier.
+ *   sync  uint32 [(batch + 1) * FCQT_SYNC_PER_SLICE] (fcqt_sizes.sync
+ *         bytes), 16-byte aligned, zero-filled once when allocated
+ *         (fcqt_fill_zero); every call leaves the slice counters at zero
+ *         again. Word batch * FCQT_SYNC_PER_SLICE is an error word: nonzero
+ *         after a call means a stage wait timed out or a stage ran on
+ *         another XCD than the stage it waits for, and the results are not
+ *         valid (the caller clears the word). One sync buffer per stream:
+ *         calls that overlap on one buffer race.
+ * Capturable into a hipGraph like every other entry point. Replace the
+ * reference's fwd2 / inv2 (persist2.cu:140-222, reached through
+ * FusedOctCQT.persist_fwd / persist_inv, fused.py:748-778). */
+#define FCQT_SYNC_PER_SLICE 64
 int fcqt_persist_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                           float* coef_re, float* coef_im, int layout,
-                          float* xs, float* work, int64_t batch, hipStream_t stream);
+                          float* xs, float* work, uint32_t* sync, int64_t batch, hipStream_t stream);
 int fcqt_persist_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* ovf,
                            const float* coef_re, const float* coef_im, int layout,
-                           float* f, float* work, float* y, int64_t batch, hipStream_t stream);
+                           float* f, float* work, float* y, uint32_t* sync, int64_t batch, hipStream_t stream);
 
 /* Allocation-free analysis: fcqt_analysis with the spectrum X and the work
  * buffer taken from a static device array of the library (each GPU holds its

@@ -73,9 +73,9 @@ int main(int argc, char** argv) {
         CHECK(fcqt_workspace_sizes(&t2, 64, &sz) == FCQT_OK);
         printf("image ok: %lld device bytes, ncoef %lld, %d tasks\n", (long long)info.device_bytes,
                (long long)info.ncoef, (int)info.ntasks);
-        printf("batch 64 bytes: signal %lld spectrum %lld work %lld scatter %lld coef_plane %lld tail %lld\n",
+        printf("batch 64 bytes: signal %lld spectrum %lld work %lld scatter %lld coef_plane %lld tail %lld sync %lld\n",
                (long long)sz.signal, (long long)sz.spectrum, (long long)sz.work, (long long)sz.scatter,
-               (long long)sz.coef_plane, (long long)sz.tail);
+               (long long)sz.coef_plane, (long long)sz.tail, (long long)sz.sync);
     }
     printf("c abi check ok (ABI %d)\n", fcqt_abi_version());
     return 0;

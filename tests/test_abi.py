@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 7
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 8
 
 
 def test_status_strings(lib):

@@ -671,10 +671,11 @@ def test_reference_entry_points(fused):
 
 @pytest.mark.parametrize("B", [1, 5, 64, 130])
 def test_single_launch_directions_equal_six_launch_bitwise(fused, B):
-    """fcqt_persist_analysis / fcqt_persist_synthesis (one cooperative launch
-    per direction, grid barriers between the phases) against the six-launch
-    path, bit for bit; B = 130 has more tiles than resident workgroups, so
-    the phases' grid-stride loops run several tiles per workgroup."""
+    """fcqt_persist_analysis / fcqt_persist_synthesis (one launch per
+    direction, a slice's stages on one XCD waiting on per-slice counters)
+    against the six-launch path, bit for bit. B = 5 leaves three XCDs
+    without a slice; B = 130 has more workgroups than fit at once. After
+    every call the counters are back at zero and the error word is clear."""
     from flash_cqt import _native
     print(f"single-launch directions: batch {B}", flush=True)
     rs = np.random.RandomState(900 + B)
@@ -682,22 +683,57 @@ def test_single_launch_directions_equal_six_launch_bitwise(fused, B):
     KR, KI = fused.fwd(x)
     k = torch.complex(KR, KI).clone()
     y = fused.bwd(KR, KI).clone()
-    PR, PI = fused.persist_fwd(x)
-    assert torch.equal(torch.complex(PR, PI), k)
-    assert torch.equal(fused.persist_inv(PR, PI), y)
+    sync = fused.sync_buffer(B)
+    for _ in range(2):      # a second call starts from the counters the first left behind
+        PR, PI = fused.persist_fwd(x)
+        assert torch.equal(torch.complex(PR, PI), k)
+        assert torch.equal(fused.persist_inv(PR, PI), y)
+        torch.cuda.synchronize()
+        assert not sync.any(), "counters not returned to zero / error word set"
     if B == 5:   # the interleaved layout through the C ABI
         kc = torch.empty(B, fused.ncoef, dtype=torch.complex64, device=_dev())
         w = fused._workspace(B)
         _native.check(fused.lib.fcqt_persist_analysis(fused._ct, fused._tp["route"], x.data_ptr(), kc.data_ptr(),
                                                       None, _native.INTERLEAVED, w["X"].data_ptr(),
-                                                      w["W"].data_ptr(), B, _native.stream_handle(0)), "persist")
+                                                      w["W"].data_ptr(), sync.data_ptr(), B,
+                                                      _native.stream_handle(0)), "persist")
         yi = torch.empty(B, N, device=_dev())
         _native.check(fused.lib.fcqt_persist_synthesis(fused._ct, fused._tp["scat"], fused._tp["ovf_scat"],
                                                        kc.data_ptr(), None, _native.INTERLEAVED, w["F"].data_ptr(),
-                                                       w["W"].data_ptr(), yi.data_ptr(), B,
+                                                       w["W"].data_ptr(), yi.data_ptr(), sync.data_ptr(), B,
                                                        _native.stream_handle(0)), "persist")
         torch.cuda.synchronize()
-        assert torch.equal(kc, k) and torch.equal(yi, y)
+        assert torch.equal(kc, k) and torch.equal(yi, y) and not sync.any()
+
+
+def test_single_launch_directions_replay_in_a_graph(fused):
+    """The single-launch directions are ordinary launches: a graph of a
+    round trip through them replays to the eager result every time, with
+    eager work on the same buffers between the replays, and leaves the
+    counters clear."""
+    B = 16
+    rs = np.random.RandomState(77)
+    x = gpu(rs.standard_normal((B, N)).astype(np.float32))
+    y = fused.bwd(*fused.fwd(x)).clone()
+    fused.sync_buffer(B)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fused.persist_inv(*fused.persist_fwd(x))
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            fused.persist_inv(*fused.persist_fwd(x))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        fused._workspace(B)["XO"].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(fused._workspace(B)["XO"], y)
+        assert torch.equal(fused.bwd(*fused.fwd(x)), y)
+        torch.cuda.synchronize()
+    assert fused.sync_error(B) == 0 and not fused.sync_buffer(B).any()
 
 
 # ------------------------------------------------------------- errors
