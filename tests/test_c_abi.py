@@ -36,7 +36,9 @@ def test_c_consumer_round_trip_on_gpu(tmp_path):
     """tests/c/roundtrip.c (built by __graft_entry__.build) runs the whole
     round trip from C: table image file, checked upload, buffer sizes from
     the library, hipMalloc, analysis, synthesis. Every row reconstructs at
-    >= 125 dB and its coefficients equal the package's bit for bit."""
+    >= 125 dB and its coefficients equal the package's bit for bit; the
+    single-launch entry points give the same bits and leave their stage
+    counters clear."""
     import numpy as np
     import torch
     from flash_cqt import OctCQT, tables as T
@@ -55,6 +57,7 @@ def test_c_consumer_round_trip_on_gpu(tmp_path):
     assert r.returncode == 0, r.stderr
     snrs = [float(line.split()[3]) for line in r.stdout.splitlines() if line.startswith("row ")]
     assert len(snrs) == B and min(snrs) >= 125, r.stdout
+    assert "single launch: same bits 1, counters and error word clear 1" in r.stdout, r.stdout
     eng = FusedOctCQT(cqt, dev)
     KR, KI = eng.fwd(torch.from_numpy(x).to(dev))
     k = np.frombuffer((tmp_path / "k.bin").read_bytes(), dtype=np.float32).reshape(2, B, eng.ncoef)
