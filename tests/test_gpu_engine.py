@@ -706,6 +706,30 @@ def test_single_launch_directions_equal_six_launch_bitwise(fused, B):
         assert torch.equal(kc, k) and torch.equal(yi, y) and not sync.any()
 
 
+def test_single_launch_reports_a_foreign_xcd_mark(fused):
+    """The host marks slice 0's record as if another XCD had run its first
+    stage: the waits still end normally (the counters are untouched), the
+    results are unchanged, and the waiting workgroups report the mismatch
+    in the error word (2). The record itself is cleared by the call."""
+    from flash_cqt import _native
+    B = 1
+    rs = np.random.RandomState(61)
+    x = gpu(rs.standard_normal((B, N)).astype(np.float32))
+    KR, KI = fused.fwd(x)
+    k = torch.complex(KR, KI).clone()
+    sync = fused.sync_buffer(B)
+    sync.zero_()
+    sync[48] = 1 << 5                 # slice 0's XCD mark: a bit of another XCD than the one running it
+    PR, PI = fused.persist_fwd(x)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.complex(PR, PI), k)
+    assert fused.sync_error(B) == 2
+    assert not sync[:B * _native.SYNC_PER_SLICE].any()
+    sync.zero_()
+    fused.persist_fwd(x)
+    assert fused.sync_error(B) == 0
+
+
 def test_single_launch_directions_replay_in_a_graph(fused):
     """The single-launch directions are ordinary launches: a graph of a
     round trip through them replays to the eager result every time, with
