@@ -152,7 +152,10 @@ class FusedOctCQT:
 
     def sync_error(self, B):
         """The single-launch error word for batch B (0: every stage wait ended
-        in time and on the right XCD). Reads device memory: synchronizes."""
+        in time and on the right XCD). Reads device memory: synchronizes.
+        After a nonzero word the failed call may have left slice counters
+        set: zero the whole buffer (`sync_buffer(B).zero_()`) before the
+        next single-launch call."""
         return int(self.sync_buffer(B)[B * _native.SYNC_PER_SLICE].item())
 
     def _fbuf(self, table, B):

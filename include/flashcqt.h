@@ -240,8 +240,9 @@ int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
  *         again. Word batch * FCQT_SYNC_PER_SLICE is an error word: nonzero
  *         after a call means a stage wait timed out or a stage ran on
  *         another XCD than the stage it waits for, and the results are not
- *         valid (the caller clears the word). One sync buffer per stream:
- *         calls that overlap on one buffer race.
+ *         valid; the failed call may also leave slice counters set, so the
+ *         caller zero-fills the whole buffer again before the next call.
+ *         One sync buffer per stream: calls that overlap on one buffer race.
  * Capturable into a hipGraph like every other entry point. Replace the
  * reference's fwd2 / inv2 (persist2.cu:140-222, reached through
  * FusedOctCQT.persist_fwd / persist_inv, fused.py:748-778). */
