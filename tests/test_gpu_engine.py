@@ -707,10 +707,12 @@ def test_single_launch_directions_equal_six_launch_bitwise(fused, B):
 
 
 def test_single_launch_reports_a_foreign_xcd_mark(fused):
-    """The host marks slice 0's record as if another XCD had run its first
+    """The host marks slice 0's record as if other XCDs had run its first
     stage: the waits still end normally (the counters are untouched), the
     results are unchanged, and the waiting workgroups report the mismatch
-    in the error word (2). The record itself is cleared by the call."""
+    in the error word (2). The record itself is cleared by the call. The
+    mark holds two XCD bits, so it differs from the running XCD's single
+    bit whichever hardware XCD id the slice lands on."""
     from flash_cqt import _native
     B = 1
     rs = np.random.RandomState(61)
@@ -719,7 +721,7 @@ def test_single_launch_reports_a_foreign_xcd_mark(fused):
     k = torch.complex(KR, KI).clone()
     sync = fused.sync_buffer(B)
     sync.zero_()
-    sync[48] = 1 << 5                 # slice 0's XCD mark: a bit of another XCD than the one running it
+    sync[48] = (1 << 5) | (1 << 6)    # slice 0's XCD mark: at least one bit of another XCD
     PR, PI = fused.persist_fwd(x)
     torch.cuda.synchronize()
     assert torch.equal(torch.complex(PR, PI), k)
