@@ -6,7 +6,9 @@
 // the shared FFT engine (M/16 threads, 16 values each). Tasks come from a
 // host-built table {M, first coefficient, band count, first band}; the grid
 // is tasks x batch, spread so that each XCD gets a contiguous range of
-// (task, slice) pairs and so reads each task's record rows from one L2.
+// (task, slice) pairs (band_place): task-major for small batches (each XCD
+// reads few tasks' record rows), slice-major from kBandSliceMajorMinBatch
+// slices on (each XCD holds whole slices, the ones whose pass tiles it ran).
 //
 // Both engines read their per-tap records in kernel order: the table holds,
 // for every task, 16 rows of 128 8-byte records, row s giving slot s of each
@@ -35,31 +37,33 @@
 
 namespace fcqt {
 
-template <int LAYOUT, bool WT>
+template <int LAYOUT, bool WT, bool SM>
 __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __restrict__ xs,
                                                               float* __restrict__ cre,
                                                               float* __restrict__ cim,
                                                               const int2* __restrict__ rec,
                                                               const int4* __restrict__ tasks, int batch,
                                                               long ncoef, const SliceMap sm,
-                                                              const float2* __restrict__ tws) {
+                                                              const float2* __restrict__ tws,
+                                                              int ntasks) {
     __shared__ float2 lds[kBandTaskLds];
     int task_id, b;
-    decode_task<false>(batch, task_id, b);
+    decode_task<false, SM>(batch, ntasks, task_id, b);
     route_task<LAYOUT, WT>(task_id, b, xs, cre, cim, rec, tasks, batch, ncoef, sm, tws, lds);
 }
 
-template <int LAYOUT, bool WT>
+template <int LAYOUT, bool WT, bool SM>
 __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __restrict__ cre,
                                                                 const float* __restrict__ cim,
                                                                 float* __restrict__ f,
                                                                 const int2* __restrict__ scat,
                                                                 const int4* __restrict__ tasks, int batch,
                                                                 long ncoef, const SliceMap sm,
-                                                                const float2* __restrict__ tws) {
+                                                                const float2* __restrict__ tws,
+                                                                int ntasks) {
     __shared__ float2 lds[kBandTaskLds];
     int task_id, b;
-    decode_task<true>(batch, task_id, b);
+    decode_task<true, SM>(batch, ntasks, task_id, b);
     scatter_task<LAYOUT, WT>(task_id, b, cre, cim, f, scat, tasks, batch, ncoef, sm, tws, lds);
 }
 
@@ -69,17 +73,28 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
 // at 1 and 2 slices. The values stored are the same.
 constexpr int64_t kBandWriteThroughMinBatch = 4;
 
+// From this batch size on the band grids run slice-major (band_place):
+// measured round trips (stream launches) at B = 64 / 96 / 128 / 192 / 256:
+// 74.0-74.3 / 99.1 / 154.5 / 243 / 337 us against 74.4-74.5 / 105.1 / 166.7 /
+// 270.4 / 367.9 us task-major; task-major stays faster at B = 16 (35.5
+// against 36.9 us). Same results either way.
+constexpr int64_t kBandSliceMajorMinBatch = 64;
+
 template <int LAYOUT>
 static void launch_route(int64_t ntasks, int64_t batch, hipStream_t stream, const float2* xs, float* cre,
                          float* cim, const int2* rec, const int4* tasks, long ncoef, const SliceMap& sm,
                          const float2* tws) {
     const dim3 grid((unsigned)(ntasks * batch));
-    if (batch >= kBandWriteThroughMinBatch)
-        hipLaunchKernelGGL((k_route_bands<LAYOUT, true>), grid, dim3(kBandThreads), 0, stream, xs, cre, cim, rec,
-                           tasks, (int)batch, ncoef, sm, tws);
+    static_assert(kBandSliceMajorMinBatch >= kBandWriteThroughMinBatch, "slice-major grids write through");
+    if (batch >= kBandSliceMajorMinBatch)
+        hipLaunchKernelGGL((k_route_bands<LAYOUT, true, true>), grid, dim3(kBandThreads), 0, stream, xs, cre, cim,
+                           rec, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
+    else if (batch >= kBandWriteThroughMinBatch)
+        hipLaunchKernelGGL((k_route_bands<LAYOUT, true, false>), grid, dim3(kBandThreads), 0, stream, xs, cre, cim,
+                           rec, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
     else
-        hipLaunchKernelGGL((k_route_bands<LAYOUT, false>), grid, dim3(kBandThreads), 0, stream, xs, cre, cim, rec,
-                           tasks, (int)batch, ncoef, sm, tws);
+        hipLaunchKernelGGL((k_route_bands<LAYOUT, false, false>), grid, dim3(kBandThreads), 0, stream, xs, cre, cim,
+                           rec, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
 }
 
 template <int LAYOUT>
@@ -87,12 +102,15 @@ static void launch_scatter(int64_t ntasks, int64_t batch, hipStream_t stream, co
                            float* f, const int2* scat, const int4* tasks, long ncoef, const SliceMap& sm,
                            const float2* tws) {
     const dim3 grid((unsigned)(ntasks * batch));
-    if (batch >= kBandWriteThroughMinBatch)
-        hipLaunchKernelGGL((k_scatter_bands<LAYOUT, true>), grid, dim3(kBandThreads), 0, stream, cre, cim, f, scat,
-                           tasks, (int)batch, ncoef, sm, tws);
+    if (batch >= kBandSliceMajorMinBatch)
+        hipLaunchKernelGGL((k_scatter_bands<LAYOUT, true, true>), grid, dim3(kBandThreads), 0, stream, cre, cim, f,
+                           scat, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
+    else if (batch >= kBandWriteThroughMinBatch)
+        hipLaunchKernelGGL((k_scatter_bands<LAYOUT, true, false>), grid, dim3(kBandThreads), 0, stream, cre, cim, f,
+                           scat, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
     else
-        hipLaunchKernelGGL((k_scatter_bands<LAYOUT, false>), grid, dim3(kBandThreads), 0, stream, cre, cim, f, scat,
-                           tasks, (int)batch, ncoef, sm, tws);
+        hipLaunchKernelGGL((k_scatter_bands<LAYOUT, false, false>), grid, dim3(kBandThreads), 0, stream, cre, cim, f,
+                           scat, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
 }
 
 }  // namespace fcqt

@@ -166,13 +166,14 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
 // REVERSE: walk each XCD's range from its end (the scatter follows the
 // route kernel on the same (task, slice) grid, so it starts with the
 // coefficients the route kernel wrote last; measured 0.2-0.9 us per round
-// trip at B = 16-120, same results).
-template <bool REVERSE>
-__device__ __forceinline__ void decode_task(int batch, int& task, int& b) {
+// trip at B = 16-120, same results). SLICE_MAJOR: the order band_place
+// describes (the launchers choose it by batch size); ntasks is the task
+// count of the grid.
+template <bool REVERSE, bool SLICE_MAJOR>
+__device__ __forceinline__ void decode_task(int batch, int ntasks, int& task, int& b) {
     const int lg = REVERSE ? xcd_remap_reverse((int)blockIdx.x, (int)gridDim.x)
                            : xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    task = lg / batch;
-    b = lg - task * batch;
+    band_place(lg, ntasks, batch, SLICE_MAJOR, task, b);
 }
 
 // LDS of a band task (float2 elements): the units, then the twiddle block.

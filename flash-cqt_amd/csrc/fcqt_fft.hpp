@@ -423,4 +423,22 @@ __host__ __device__ __forceinline__ int xcd_remap_reverse(int lin, int G) {
     return start + (n - 1 - idx);
 }
 
+// Logical band workgroup lg of a grid of ntasks x batch -> (task, slice b).
+// Task-major (lg = task * batch + b): each XCD's contiguous range holds a few
+// tasks of every slice, so it reads few tasks' record rows. Slice-major
+// (lg = b * ntasks + task): each XCD's range holds whole slices, the same
+// slices whose pass tiles xcd_remap put on that XCD, so a slice's spectrum
+// and slot rows stay with one L2 and the record rows are shared by its
+// slices. Bijective on [0, ntasks * batch) either way.
+__host__ __device__ __forceinline__ void band_place(int lg, int ntasks, int batch, bool slice_major, int& task,
+                                                    int& b) {
+    if (slice_major) {
+        b = lg / ntasks;
+        task = lg - b * ntasks;
+    } else {
+        task = lg / batch;
+        b = lg - task * batch;
+    }
+}
+
 }  // namespace fcqt

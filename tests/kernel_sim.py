@@ -539,3 +539,11 @@ def xcd_remap_reverse(lin, G):
     n = q + 1 if x < rem else q
     start = x * (q + 1) if x < rem else rem * (q + 1) + (x - rem) * q
     return start + (n - 1 - i)
+
+
+def band_place(lg, ntasks, batch, slice_major):
+    """fcqt_fft.hpp band_place: logical band workgroup -> (task, slice),
+    task-major (lg = task * batch + b) or slice-major (lg = b * ntasks + task)."""
+    if slice_major:
+        return lg % ntasks, lg // ntasks
+    return lg // batch, lg % batch

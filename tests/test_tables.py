@@ -421,3 +421,42 @@ def test_xcd_map_replicas_equal_the_kernels_maps_cpu(tmp_path):
         assert vals[0] == G
         assert vals[1:] == [ks.xcd_remap(l, G) for l in range(G)]
         assert [int(v) for v in rev.split()] == [ks.xcd_remap_reverse(l, G) for l in range(G)]
+
+
+def test_band_orders_match_the_kernels_and_keep_slices_on_one_xcd_cpu(tmp_path):
+    """band_place, compiled for the host from fcqt_fft.hpp, equals the
+    simulator's replica under both orders; each order covers every (task,
+    slice) once; and slice-major puts whole slices on each XCD of the band
+    grid (xcd_remap ranges) at the batch sizes where the launchers use it,
+    the same slices xcd_remap gives that XCD in the wide pass grids."""
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not pathlib.Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    exe = tmp_path / "xcd_maps"
+    r = subprocess.run([hipcc, "-O1", "-std=c++17", "--offload-arch=gfx950", str(ROOT / "tests" / "c" / "xcd_maps.hip"),
+                        "-o", str(exe)], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    nt = 68
+    for B in (1, 5, 16, 64, 128):
+        out = subprocess.run([str(exe), "band", str(nt), str(B)], capture_output=True, text=True, timeout=120)
+        assert out.returncode == 0, out.stderr
+        lines = out.stdout.strip().splitlines()
+        assert len(lines) == 2
+        for order, ln in enumerate(lines):
+            got = [tuple(int(v) for v in p.split(",")) for p in ln.split()]
+            want = [ks.band_place(lg, nt, B, order == 1) for lg in range(nt * B)]
+            assert got == want
+            assert sorted(got) == sorted((t, b) for t in range(nt) for b in range(B))
+    for B in (64, 128, 256):
+        G = nt * B
+        per_xcd = {}
+        for lin in range(G):
+            t, b = ks.band_place(ks.xcd_remap(lin, G), nt, B, True)
+            per_xcd.setdefault(lin & 7, set()).add(b)
+        pass_xcd = {}
+        for lin in range(8 * B):           # wide row pass: 8 workgroups per slice
+            pass_xcd.setdefault(lin & 7, set()).add(ks.xcd_remap(lin, 8 * B) // 8)
+        for x in range(8):
+            assert per_xcd[x] == pass_xcd[x] == set(range(x * B // 8, (x + 1) * B // 8))
