@@ -515,7 +515,7 @@ def kernel_timings(f, B, reps):
 # kernel names in the profiles (the pass kernels in their wide tile shapes
 # and the band kernels with write-through stores, which batch 64 runs)
 KERNEL_SYMBOL = {"packed_fft": ("k_col_fwd<false,16>", "k_row_fwd<16>"), "route_bands": ("k_route_bands<0,true,true>",),
-                 "scatter_bands": ("k_scatter_bands<0,true,true>",), "packed_ifft": ("k_col_inv<32>", "k_row_inv<16>")}
+                 "scatter_bands": ("k_scatter_bands<0,true,true>",), "packed_ifft": ("k_col_inv<32,true>", "k_row_inv<16,true>")}
 
 
 def measured_traffic(name, B):

@@ -70,8 +70,15 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
 // From this batch size on the band kernels write their outputs through the
 // L2 (store_out<true>): measured faster from 4 slices up (B = 4: route 5.14
 // against 5.39 us; B = 24: scatter 8.8 against 10.8 us) and slightly slower
-// at 1 and 2 slices. The values stored are the same.
+// at 1 and 2 slices. Above kBandWriteThroughMaxBatch the round trip's working
+// set no longer fits the memory-side cache and plain stores win again
+// (slice-major round trips, write-through against plain in both band
+// kernels: B = 80 87.1-87.7 against 88.1, B = 96 98.2-98.4 against 98.9-99.6,
+// B = 112 130.2-130.4 against 120.6-120.9, B = 128 155.2-155.4 against 143.6,
+// B = 192 244.3 against 223.2-223.5, B = 256 336.0 against 314.9-315.1 us).
+// The values stored are the same.
 constexpr int64_t kBandWriteThroughMinBatch = 4;
+constexpr int64_t kBandWriteThroughMaxBatch = 104;
 
 // From this batch size on the band grids run slice-major (band_place):
 // measured round trips (stream launches) at B = 64 / 96 / 128 / 192 / 256:
@@ -85,8 +92,14 @@ static void launch_route(int64_t ntasks, int64_t batch, hipStream_t stream, cons
                          float* cim, const int2* rec, const int4* tasks, long ncoef, const SliceMap& sm,
                          const float2* tws) {
     const dim3 grid((unsigned)(ntasks * batch));
-    static_assert(kBandSliceMajorMinBatch >= kBandWriteThroughMinBatch, "slice-major grids write through");
-    if (batch >= kBandSliceMajorMinBatch)
+    static_assert(kBandWriteThroughMinBatch <= kBandSliceMajorMinBatch &&
+                      kBandSliceMajorMinBatch <= kBandWriteThroughMaxBatch,
+                  "batch ranges: plain task-major, write-through task-major, write-through slice-major, "
+                  "plain slice-major");
+    if (batch > kBandWriteThroughMaxBatch)
+        hipLaunchKernelGGL((k_route_bands<LAYOUT, false, true>), grid, dim3(kBandThreads), 0, stream, xs, cre, cim,
+                           rec, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
+    else if (batch >= kBandSliceMajorMinBatch)
         hipLaunchKernelGGL((k_route_bands<LAYOUT, true, true>), grid, dim3(kBandThreads), 0, stream, xs, cre, cim,
                            rec, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
     else if (batch >= kBandWriteThroughMinBatch)
@@ -102,7 +115,10 @@ static void launch_scatter(int64_t ntasks, int64_t batch, hipStream_t stream, co
                            float* f, const int2* scat, const int4* tasks, long ncoef, const SliceMap& sm,
                            const float2* tws) {
     const dim3 grid((unsigned)(ntasks * batch));
-    if (batch >= kBandSliceMajorMinBatch)
+    if (batch > kBandWriteThroughMaxBatch)
+        hipLaunchKernelGGL((k_scatter_bands<LAYOUT, false, true>), grid, dim3(kBandThreads), 0, stream, cre, cim, f,
+                           scat, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
+    else if (batch >= kBandSliceMajorMinBatch)
         hipLaunchKernelGGL((k_scatter_bands<LAYOUT, true, true>), grid, dim3(kBandThreads), 0, stream, cre, cim, f,
                            scat, tasks, (int)batch, ncoef, sm, tws, (int)ntasks);
     else if (batch >= kBandWriteThroughMinBatch)

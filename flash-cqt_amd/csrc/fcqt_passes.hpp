@@ -23,6 +23,8 @@ constexpr int kInvColsWide = 32, kInvColsNarrow = 16;
 constexpr int64_t kNarrowMaxBatch = 16;
 // the fold lists are built for the wide inverse column workgroups
 constexpr int kFoldLists = 256 / kInvColsWide;
+// the wide inverse passes write through the L2 up to this batch size
+constexpr int64_t kInvWriteThroughMaxBatch = 104;
 
 // ------------------------------------------------------------ column pass
 
@@ -71,10 +73,14 @@ __device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const float* 
 // Each pass is a tile body over (slice b, tile index) working in LDS the
 // caller provides (the kernels below and the single-launch kernels of
 // persist.hip run the same bodies, so both give the same bits): CPW (or RPW)
-// units, then the twiddle block. The wide shapes (the batches above
-// kNarrowMaxBatch) of the inverse passes write their outputs through the L2
-// (store_out<true>: the inverse pair ran 1.4 us faster at batch 64). The
-// forward passes and the narrow shapes use plain stores: a write-through W
+// units, then the twiddle block. The inverse passes take WT, the store form:
+// the wide shapes write through the L2 up to kInvWriteThroughMaxBatch slices
+// (store_out<true>: the inverse pair ran 1.4 us faster at batch 64) and plainly
+// above, where the round trip's working set outgrows the memory-side cache
+// (round trips 119.4-119.8 against 120.6-121.1 us at B = 112, 142.9-143.1
+// against 145.9 us at B = 128, 308.4-308.6 against 314.0 us at B = 256; 101
+// against 98.2-98.7 us at B = 96). The forward passes and the narrow shapes
+// use plain stores: a write-through W
 // is no longer in the L2 when the row pass of the same slice reads it on
 // the same XCD (its hit rate fell from 0.53 to 0.06, and the round trip
 // was 0.4 us slower), and the forward row pass covers each 128-byte line of
@@ -151,7 +157,7 @@ __device__ __forceinline__ int inv_col(int w, int c) {
     return c < H ? p : (p == 0 ? 128 : 256 - p);
 }
 
-template <int CPW>
+template <int CPW, bool WT>
 __device__ __forceinline__ void col_inv_tile(const int b, const int w, const float2* __restrict__ f,
                                              float2* __restrict__ out, const float2* __restrict__ twp,
                                              const float2* __restrict__ twn, const int* __restrict__ fold,
@@ -268,7 +274,7 @@ __device__ __forceinline__ void col_inv_tile(const int b, const int w, const flo
 #pragma unroll
         for (int r = 0; r < P::RL; ++r) {
             const int k1 = t + 8 * q + 16 * r;
-            store_out<CPW == kInvColsWide>(&yb[k1 * 256 + col], cmul(v[q * P::RL + r], tp[q * P::RL + r]));
+            store_out<WT>(&yb[k1 * 256 + col], cmul(v[q * P::RL + r], tp[q * P::RL + r]));
         }
     }
 }
@@ -366,7 +372,7 @@ __device__ __forceinline__ void row_fwd_tile(const int b, const int w, const flo
 }
 
 
-template <int RPW>
+template <int RPW, bool WT>
 __device__ __forceinline__ void row_inv_tile(const int b, const int rg, const float2* __restrict__ in,
                                              float2* __restrict__ y, const float2* __restrict__ tws, float2* lds) {
     using P = Plan<256>;
@@ -385,7 +391,7 @@ __device__ __forceinline__ void row_inv_tile(const int b, const int rg, const fl
     for (int u = 0; u < 16; ++u) {
         const int k2 = kg + 16 * u;
         const float2 w = s2[pad16(k2)];
-        store_out<RPW == kRowsWide>(&yo[kk1 + 128 * k2], make_float2(w.x * sc, -w.y * sc));
+        store_out<WT>(&yo[kk1 + 128 * k2], make_float2(w.x * sc, -w.y * sc));
     }
 }
 

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(8 * CPW) void k_col_fwd(const float2* __restrict__ 
     col_fwd_tile<SLICED, CPW>(b, lg - b * kWgs, in, out, twp, tws, src, lds);
 }
 
-template <int CPW>
+template <int CPW, bool WT>
 __global__ __launch_bounds__(8 * CPW) void k_col_inv(const float2* __restrict__ f, float2* __restrict__ out,
                                                      const float2* __restrict__ twp,
                                                      const float2* __restrict__ twn,
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(8 * CPW) void k_col_inv(const float2* __restrict__ 
     __shared__ float2 lds[col_lds<CPW>()];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int b = lg / kWgs;
-    col_inv_tile<CPW>(b, lg - b * kWgs, f, out, twp, twn, fold, tws, lds);
+    col_inv_tile<CPW, WT>(b, lg - b * kWgs, f, out, twp, twn, fold, tws, lds);
 }
 
 template <int RPW>
@@ -64,14 +64,14 @@ __global__ __launch_bounds__(16 * RPW) void k_row_fwd(const float2* __restrict__
     row_fwd_tile<RPW>(b, lg - b * kWgs, in, xs, twn, tws, lds);
 }
 
-template <int RPW>
+template <int RPW, bool WT>
 __global__ __launch_bounds__(16 * RPW) void k_row_inv(const float2* __restrict__ in, float2* __restrict__ y,
                                                       const float2* __restrict__ tws) {
     constexpr int kWgs = 128 / RPW;               // workgroups per slice
     __shared__ float2 lds[row_lds<RPW>()];
     const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int b = lg / kWgs;
-    row_inv_tile<RPW>(b, lg - b * kWgs, in, y, tws, lds);
+    row_inv_tile<RPW, WT>(b, lg - b * kWgs, in, y, tws, lds);
 }
 
 // Launch helpers: the pass kernels of one direction in the tile shape the
@@ -97,13 +97,13 @@ static int fwd_passes(const float2* x, float2* work, float2* xs, const float2* t
     return launch_fwd_passes<kColsWide, kRowsWide>(x, work, xs, twp, twh, tws, src, sliced, batch, stream);
 }
 
-template <int CPW, int RPW>
+template <int CPW, int RPW, bool WT>
 static int launch_inv_passes(const float2* f, float2* work, float2* y, const float2* twp, const float2* twh,
                              const int* ovf, const float2* tws, int64_t batch, hipStream_t stream) {
-    hipLaunchKernelGGL((k_col_inv<CPW>), dim3((unsigned)(batch * (256 / CPW))), dim3(8 * CPW), 0, stream, f, work,
-                       twp, twh, ovf, tws);
+    hipLaunchKernelGGL((k_col_inv<CPW, WT>), dim3((unsigned)(batch * (256 / CPW))), dim3(8 * CPW), 0, stream, f,
+                       work, twp, twh, ovf, tws);
     if (int e = launch_status()) return e;
-    hipLaunchKernelGGL((k_row_inv<RPW>), dim3((unsigned)(batch * (128 / RPW))), dim3(16 * RPW), 0, stream, work,
+    hipLaunchKernelGGL((k_row_inv<RPW, WT>), dim3((unsigned)(batch * (128 / RPW))), dim3(16 * RPW), 0, stream, work,
                        y, tws);
     return launch_status();
 }
@@ -111,8 +111,10 @@ static int launch_inv_passes(const float2* f, float2* work, float2* y, const flo
 static int inv_passes(const float2* f, float2* work, float2* y, const float2* twp, const float2* twh, const int* ovf,
                       const float2* tws, int64_t batch, hipStream_t stream) {
     if (batch <= kNarrowMaxBatch)
-        return launch_inv_passes<kInvColsNarrow, kRowsNarrow>(f, work, y, twp, twh, ovf, tws, batch, stream);
-    return launch_inv_passes<kInvColsWide, kRowsWide>(f, work, y, twp, twh, ovf, tws, batch, stream);
+        return launch_inv_passes<kInvColsNarrow, kRowsNarrow, false>(f, work, y, twp, twh, ovf, tws, batch, stream);
+    if (batch <= kInvWriteThroughMaxBatch)
+        return launch_inv_passes<kInvColsWide, kRowsWide, true>(f, work, y, twp, twh, ovf, tws, batch, stream);
+    return launch_inv_passes<kInvColsWide, kRowsWide, false>(f, work, y, twp, twh, ovf, tws, batch, stream);
 }
 
 }  // namespace fcqt

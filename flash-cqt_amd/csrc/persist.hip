@@ -195,12 +195,12 @@ __global__ __launch_bounds__(kFlowThreads) void k_flow_synthesis(const FlowArgs 
         flow_signal(rec, kSyncStage1, true);
     } else if (stage == 2) {
         flow_wait(rec, kSyncStage1, (unsigned)p.ntasks, err);
-        col_inv_tile<kFInvColsPerTile>(b, t, reinterpret_cast<const float2*>(p.f), p.work, p.twp, p.twh, p.ovf,
+        col_inv_tile<kFInvColsPerTile, false>(b, t, reinterpret_cast<const float2*>(p.f), p.work, p.twp, p.twh, p.ovf,
                                        p.tws, lds);
         flow_signal(rec, kSyncStage2, false);
     } else {
         flow_wait(rec, kSyncStage2, kFInvColTiles, err);
-        row_inv_tile<kFRowsPerTile>(b, t, p.work, p.y, p.tws, lds);
+        row_inv_tile<kFRowsPerTile, false>(b, t, p.work, p.y, p.tws, lds);
         flow_finish(rec, kFRowTiles);
     }
 }
