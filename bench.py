@@ -535,15 +535,28 @@ def measured_traffic(name, B):
     return sum(got[s] for s in syms) / len(syms)
 
 
-def kernels_only(f, B, reps):
+def kernels_only(f, B, reps, band_tasks=None):
     """A few launches of each kernel and one plain copy of known size, for
-    rocprofv3 --pmc runs (FETCH_SIZE / WRITE_SIZE calibration)."""
+    rocprofv3 --pmc runs (FETCH_SIZE / WRITE_SIZE calibration). With
+    band_tasks = K only the two band kernels run, on the first K tasks."""
     from flash_cqt import _native
     dev = f.dev
     w = f._workspace(B)
     x = randn(B, 1).to(dev)
     kr, ki = w["KR"], w["KI"]          # the engine's own coefficient planes (their placement matters)
     y = torch.empty(B, N, device=dev)
+    if band_tasks:
+        t, k = leading_tasks(f, ntasks=band_tasks)
+        sh = _native.stream_handle(dev.index)
+        f.packed_fft(x, w["X"], w["W"])
+        for _ in range(reps):
+            _native.check(f.lib.fcqt_route_bands(t, f._tp["route"], w["X"].data_ptr(), kr.data_ptr(), ki.data_ptr(),
+                                                 _native.PLANAR, B, sh), "route_bands")
+            _native.check(f.lib.fcqt_scatter_bands(t, f._tp["scat"], kr.data_ptr(), ki.data_ptr(), _native.PLANAR,
+                                                   w["F"].data_ptr(), B, sh), "scatter_bands")
+        torch.cuda.synchronize()
+        log(f"kernels-only: B={B} reps={reps}; band kernels on the first {k} tasks")
+        return
     src = torch.ones(16 * 1024 * 1024, device=dev)      # 64 MiB
     dst = torch.empty_like(src)
     for _ in range(reps):
@@ -554,6 +567,77 @@ def kernels_only(f, B, reps):
         dst.copy_(src)
     torch.cuda.synchronize()
     log(f"kernels-only: B={B} reps={reps}; copy kernel moves 64 MiB read + 64 MiB write per launch")
+
+
+def leading_tasks(f, max_m=None, ntasks=None):
+    """A copy of the engine's table descriptor whose task table is cut to its
+    first tasks: the first `ntasks`, or the leading tasks of band length
+    <= max_m. Returns (descriptor, task count)."""
+    import ctypes
+    from flash_cqt import _native
+    if ntasks is None:
+        ms = f.tables["tasks"][:, 0].cpu().tolist()
+        ntasks = 0
+        while ntasks < len(ms) and ms[ntasks] <= max_m:
+            ntasks += 1
+    t = _native.Tables()
+    ctypes.memmove(ctypes.addressof(t), ctypes.addressof(f._ct), ctypes.sizeof(t))
+    t.ntasks = ntasks
+    return t, ntasks
+
+
+def band_exchange(f, batches=(16, 64), reps=20):
+    """The two stage exchanges of the small band units (M <= 256): the
+    library's LDS exchange against the cross-lane (DPP) exchange of the
+    variant library libflashcqt_xlane.so. Both band kernels run on the
+    leading tasks of M <= 256 only (the tasks the variant changes), on the
+    same buffers, hipEvents around `reps` back-to-back launches (median of 7,
+    the two libraries alternating), and their coefficients and slot buffers
+    are compared bit for bit."""
+    from flash_cqt import _native
+    dev = f.dev
+    libs = {"lds": f.lib, "cross_lane": _native.load_variant("xlane")}
+    t, k = leading_tasks(f, max_m=256)
+    sh = _native.stream_handle(dev.index)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    out = {"tasks": k, "band_lengths": sorted(set(f.tables["tasks"][:k, 0].cpu().tolist())),
+           "duration_source": f"hipEvents around {reps} back-to-back launches, median of 7"}
+    for B in batches:
+        w = f._workspace(B)
+        x = randn(B, 2).to(dev)
+        f.packed_fft(x, w["X"], w["W"])
+        kr, ki, F = w["KR"], w["KI"], w["F"]
+        res, bits = {}, {}
+        for name, lib in libs.items():
+            calls = {
+                "route": lambda lib=lib: lib.fcqt_route_bands(t, f._tp["route"], w["X"].data_ptr(), kr.data_ptr(),
+                                                              ki.data_ptr(), _native.PLANAR, B, sh),
+                "scatter": lambda lib=lib: lib.fcqt_scatter_bands(t, f._tp["scat"], kr.data_ptr(), ki.data_ptr(),
+                                                                  _native.PLANAR, F.data_ptr(), B, sh),
+            }
+            for cn, fn in calls.items():
+                _native.check(fn(), cn)
+            torch.cuda.synchronize()
+            bits[name] = (kr.clone(), ki.clone(), F.clone())
+            for cn, fn in calls.items():
+                ts = []
+                for _ in range(7):
+                    fn()
+                    a.record()
+                    for _ in range(reps):
+                        fn()
+                    b.record()
+                    b.synchronize()
+                    ts.append(a.elapsed_time(b) / reps * 1e3)
+                ts.sort()
+                res[f"{cn}_{name}_us"] = ts[3]
+        res["bitwise_equal"] = all(torch.equal(p, q) for p, q in zip(bits["lds"], bits["cross_lane"]))
+        out[str(B)] = res
+        log(f"band exchange B={B} ({k} tasks, M <= 256): " + ", ".join(
+            f"{key} {val:.2f}" for key, val in res.items() if key.endswith("_us"))
+            + f", bitwise equal {res['bitwise_equal']}")
+    return out
 
 
 # ------------------------------------------------------------------ main
@@ -573,6 +657,11 @@ def main():
                     help="skip the single-launch (cooperative) directions")
     ap.add_argument("--single-launch-only", action="store_true",
                     help="time only the single-launch directions and the per-launch floor; print their JSON")
+    ap.add_argument("--band-tasks", type=int, default=None,
+                    help="with --kernels-only: run only the band kernels, on the first K tasks")
+    ap.add_argument("--lib-variant", choices=("xlane",), default=None,
+                    help="with --kernels-only: launch from a variant library (xlane: cross-lane exchange of the "
+                         "band units of M <= 256)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -598,7 +687,10 @@ def main():
         print(json.dumps(json_safe(single_launch_workload(f, dev))), flush=True)
         return
     if args.kernels_only:
-        kernels_only(f, args.batch, max(1, args.kernel_reps // 4))
+        if args.lib_variant:
+            from flash_cqt import _native
+            f.lib = _native.load_variant(args.lib_variant)
+        kernels_only(f, args.batch, max(1, args.kernel_reps // 4), args.band_tasks)
         return
 
     batches = sorted({1, 16, 64, args.batch})
@@ -693,6 +785,7 @@ def main():
                "traffic_source": "sum over the six kernels in profiles/hbm_traffic_b64.txt" if rt_traffic else None}
 
     sliced = sliced_workload(dev)
+    exchange = band_exchange(f)
     train = training_step(dev, cqt_gpu)
     mem = peak_memory(cqt_gpu, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(batch=B)
@@ -712,6 +805,7 @@ def main():
         "per_batch": {str(k): v for k, v in per_batch.items()},
         "kernels": kern,
         "sliced": sliced,
+        "band_exchange": exchange,
         "training_step": train,
         "table_bytes": f.table_bytes,
         "roofline": roof,

@@ -2,7 +2,10 @@
 
     python flash-cqt_amd/build.py [--verbose]
 
-Output: flash-cqt_amd/flash_cqt/_lib/libflashcqt.so. Flags: -O3 for gfx950,
+Output: flash-cqt_amd/flash_cqt/_lib/libflashcqt.so, and beside it the
+variant library libflashcqt_xlane.so (the same sources with the band units of
+M <= 256 exchanging across lanes instead of through LDS; the benchmark and the
+GPU tests compare the two). Both compile in parallel. Flags: -O3 for gfx950,
 packed fp32 instructions disabled (-Xclang -target-feature -Xclang
 -packed-fp32-ops). The host pass warns that it does not know the packed-fp32
 feature; that warning is harmless.
@@ -33,11 +36,15 @@ def hipcc():
     raise RuntimeError("hipcc not found")
 
 
-def command(out=OUT):
+# variant name -> (output, extra defines)
+VARIANTS = {"": (OUT, ()), "xlane": (OUT.with_name("libflashcqt_xlane.so"), ("-DFCQT_XLANE_MAX_M=256",))}
+
+
+def command(out=OUT, defines=()):
     return [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
             "-Rpass-analysis=kernel-resource-usage", "-Wall", "-Wno-unused-command-line-argument",
-            *[str(CSRC / s) for s in SOURCES], "-o", str(out)]
+            *defines, *[str(CSRC / s) for s in SOURCES], "-o", str(out)]
 
 
 _REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|LDS Size \[bytes/block\]|"
@@ -57,28 +64,43 @@ def resource_usage(text):
 
 
 def build(verbose=False):
+    """Compile the library and its variants (in parallel); returns the
+    library's path. Fails on a compile error or on any kernel that uses
+    scratch memory; writes the library's resource report to
+    _lib/resources.txt."""
     OUT.parent.mkdir(parents=True, exist_ok=True)
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = command(tmp)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    text = res.stdout + res.stderr
-    lines = [ln for ln in text.splitlines()
-             if "packed-fp32-ops' is not a recognized feature" not in ln and "remark:" not in ln]
-    if verbose or res.returncode != 0:
-        print(" ".join(cmd))
-        print("\n".join(lines))
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode})")
-    usage = resource_usage(text)
-    if not usage:
-        raise RuntimeError("hipcc printed no kernel resource report")
-    spilled = {k: v for k, v in usage.items() if v.get("ScratchSize", 0) > 0}
-    if spilled:
-        raise RuntimeError(f"kernels use scratch memory: {spilled}")
-    with open(OUT.parent / "resources.txt", "w") as f:
-        for k, v in sorted(usage.items()):
-            f.write(k + " " + " ".join(f"{a}={b}" for a, b in v.items()) + "\n")
-    os.replace(tmp, OUT)
+    procs = {}
+    for name, (out, defines) in VARIANTS.items():
+        tmp = out.with_suffix(".so.tmp")
+        cmd = command(tmp, defines)
+        procs[name] = (out, tmp, cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                                                       text=True))
+    failed = []
+    for name, (out, tmp, cmd, proc) in procs.items():
+        text, _ = proc.communicate()
+        lines = [ln for ln in text.splitlines()
+                 if "packed-fp32-ops' is not a recognized feature" not in ln and "remark:" not in ln]
+        if verbose or proc.returncode != 0:
+            print(" ".join(cmd))
+            print("\n".join(lines))
+        if proc.returncode != 0:
+            failed.append(f"{name or 'library'}: hipcc failed ({proc.returncode})")
+            continue
+        usage = resource_usage(text)
+        if not usage:
+            failed.append(f"{name or 'library'}: hipcc printed no kernel resource report")
+            continue
+        spilled = {k: v for k, v in usage.items() if v.get("ScratchSize", 0) > 0}
+        if spilled:
+            failed.append(f"{name or 'library'}: kernels use scratch memory: {spilled}")
+            continue
+        if not name:
+            with open(OUT.parent / "resources.txt", "w") as f:
+                for k, v in sorted(usage.items()):
+                    f.write(k + " " + " ".join(f"{a}={b}" for a, b in v.items()) + "\n")
+        os.replace(tmp, out)
+    if failed:
+        raise RuntimeError("; ".join(failed))
     return OUT
 
 

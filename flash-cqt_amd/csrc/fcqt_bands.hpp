@@ -10,6 +10,21 @@
 namespace fcqt {
 
 constexpr int kBandThreads = 128;
+
+// Band units of length M <= FCQT_XLANE_MAX_M exchange between their first
+// two stages across lanes (fft_unit_xl) instead of through LDS. 0 in the
+// library (the LDS exchange measured faster); the variant library
+// libflashcqt_xlane.so is built with 256.
+#ifndef FCQT_XLANE_MAX_M
+#define FCQT_XLANE_MAX_M 0
+#endif
+
+// The unit transform of the band kernels.
+template <int M, int SIGN>
+__device__ __forceinline__ void band_fft(float2* v, float2* s, int t, const float2* tl, const Tw3<M>& w3) {
+    if constexpr (M <= FCQT_XLANE_MAX_M) fft_unit_xl<M, SIGN>(v, t, tl);
+    else fft_unit<M, SIGN>(v, s, t, tl, w3);
+}
 constexpr int kBandPoints = 16 * kBandThreads;  // complex values (and records) per task
 
 constexpr int band_lds(int M) { return (kBandPoints / M) * (M + M / 16 + 1); }
@@ -104,7 +119,7 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
         v[r] = make_float2(fabsf(w) * x.x, w * x.y);
     }
     put_tw2<M, kBandThreads>(tw2, c2, threadIdx.x);
-    fft_unit<M, +1>(v, lds + u * P::US, t, tw2, w3);
+    band_fft<M, +1>(v, lds + u * P::US, t, tw2, w3);
     if (u < task.z) {
         long ob;
         int shift;
@@ -147,7 +162,7 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
     int2 rv[16];
     load_records(rv, scat, task_id);
     put_tw2<M, kBandThreads>(tw2, c2, threadIdx.x);
-    fft_unit<M, -1>(v, lds + u * P::US, t, tw2, w3);
+    band_fft<M, -1>(v, lds + u * P::US, t, tw2, w3);
     if (active) {
         float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
 #pragma unroll

@@ -403,6 +403,88 @@ __device__ __forceinline__ void fft_unit(float2* v, float2* s, int t, const floa
     }
 }
 
+// ------------------------------------- cross-lane (DPP) stage exchange
+// An alternative stage-1 -> 2 exchange for units of M <= 256, whose T <= 16
+// threads are consecutive, T-aligned lanes of one row of 16 lanes (the band
+// kernels' layout). After the radix-16 first stage, thread t holds output
+// k1 = t' + T q of its own column in v[T q + t']; the second stage needs, in
+// v[T q + r], output k1 = t + T q of thread r. That is a transpose of the
+// log2(T) lane bits with the low register bits, done as one butterfly level
+// per bit: a DPP read of the partner lane (lane ^ 2^P) and two selects per
+// float. The arithmetic is the LDS path's, with the same output layout.
+// Measured on MI355X (band kernels restricted to the six tasks of M <= 256,
+// 20 launches, B = 16 / 64 / 256): route 4.56 / 5.8-6.0 / 11.7 us against
+// 4.00 / 5.2 / 11.2 us with the LDS exchange, scatter 4.85 / 6.0 / 9.05 us
+// against 4.25 / 4.93 / 7.8 us; M = 32 and 64 alone: equal or up to 5%
+// slower. Each level costs about 64 VALU instructions per thread where the
+// LDS exchange issues 16 writes and 16 reads for all levels at once, and the
+// band kernels are busier on the VALU than on the LDS, so the library is
+// built with the LDS exchange and this one only in the variant library
+// (FCQT_XLANE_MAX_M = 256, libflashcqt_xlane.so) that the benchmark and the
+// tests compare against it.
+
+// Partner read for lane bit P: lanes with bit P clear read lane + 2^P
+// (ABOVE), lanes with bit P set read lane - 2^P, inside rows of 16 lanes.
+template <int P, bool ABOVE>
+__device__ __forceinline__ float dpp_partner(float x) {
+    static_assert(P >= 0 && P < 4, "lane bit inside a row of 16 lanes");
+    // quad_perm [1,0,3,2] / [2,3,0,1]; row_shl:4 / row_shr:4; row_ror:8
+    constexpr int ctrl = P == 0 ? 0xB1 : P == 1 ? 0x4E : P == 2 ? (ABOVE ? 0x104 : 0x114) : 0x128;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false));
+}
+
+// One level: lane l with bit P set exchanges its register i (bit P clear)
+// with register i | 2^P of lane l ^ 2^P.
+template <int P>
+__device__ __forceinline__ void xlane_level(float2* v, int t) {
+    const bool hi = (t >> P) & 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int i = ((k >> P) << (P + 1)) | (k & ((1 << P) - 1));
+        const int i2 = i | (1 << P);
+        float ax = v[i].x, ay = v[i].y, bx = v[i2].x, by = v[i2].y;
+        // selects on values (a select between two elements of v would become
+        // a lane-dependent index and push v out of registers)
+        asm("" : "+v"(ax), "+v"(ay), "+v"(bx), "+v"(by));
+        const float sx = hi ? ax : bx, sy = hi ? ay : by;
+        const float ux = dpp_partner<P, true>(sx), uy = dpp_partner<P, true>(sy);
+        const float dx = P == 2 ? dpp_partner<P, false>(sx) : ux;
+        const float dy = P == 2 ? dpp_partner<P, false>(sy) : uy;
+        v[i2].x = hi ? bx : ux;
+        v[i2].y = hi ? by : uy;
+        v[i].x = hi ? dx : ax;
+        v[i].y = hi ? dy : ay;
+    }
+}
+
+// Unit transform for M <= 256 with the cross-lane exchange; same contract
+// as fft_unit (entry v[r] = x[t + T r], exit v[q RL + r] = X[t + T q + r OS]),
+// tl holds the second-stage twiddle block. Every thread of the workgroup
+// calls this (one barrier: tl is written before the call).
+template <int M, int SIGN>
+__device__ __forceinline__ void fft_unit_xl(float2* v, int t, const float2* tl) {
+    constexpr int T = M / 16;
+    static_assert(T >= 2 && T <= 16 && Plan<M>::R3 == 1 && Plan<M>::R2 == T, "cross-lane units");
+    dft16<SIGN>(v);
+    xlane_level<0>(v, t);
+    if constexpr (T >= 4) xlane_level<1>(v, t);
+    if constexpr (T >= 8) xlane_level<2>(v, t);
+    if constexpr (T >= 16) xlane_level<3>(v, t);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 16 / T; ++q) {
+        const float2* tk = tl + ((t + T * q) & 15);
+        float2 a[T];
+#pragma unroll
+        for (int r = 0; r < T; ++r) a[r] = v[q * T + r];
+#pragma unroll
+        for (int r = 1; r < T; ++r) a[r] = SIGN < 0 ? cmul(a[r], tk[16 * r]) : cmulc(a[r], tk[16 * r]);
+        dft<T, SIGN>(a);
+#pragma unroll
+        for (int r = 0; r < T; ++r) v[q * T + r] = a[r];
+    }
+}
+
 // Spread consecutive workgroup ids over the 8 XCDs' L2s so that each XCD
 // receives a contiguous range of logical ids (the hardware dispatches ids
 // round-robin over XCDs). Bijective on [0, G).

@@ -56,6 +56,9 @@ class NativeError(RuntimeError):
 
 
 _lib = None
+_variants = {}
+#: variant libraries (same C ABI, other kernel builds): name -> file in _lib/
+VARIANTS = {"xlane": "libflashcqt_xlane.so"}
 
 
 def load():
@@ -63,13 +66,30 @@ def load():
     global _lib
     if _lib is not None:
         return _lib
-    if not LIB_PATH.exists():
-        raise NativeError(f"flash_cqt HIP library not built ({LIB_PATH}); "
+    _lib = _open(LIB_PATH)
+    return _lib
+
+
+def load_variant(name):
+    """Load and type a variant library built beside the library (its C ABI
+    is the library's): "xlane" runs the band units of M <= 256 with the
+    cross-lane exchange between their first two stages. Raises NativeError
+    if it is not built."""
+    if name not in _variants:
+        if name not in VARIANTS:
+            raise NativeError(f"unknown library variant {name!r}")
+        _variants[name] = _open(LIB_PATH.with_name(VARIANTS[name]))
+    return _variants[name]
+
+
+def _open(path):
+    if not path.exists():
+        raise NativeError(f"flash_cqt HIP library not built ({path}); "
                           "run __graft_entry__.build()")
     try:
-        lib = ctypes.CDLL(str(LIB_PATH))
+        lib = ctypes.CDLL(str(path))
     except OSError as e:
-        raise NativeError(f"cannot load {LIB_PATH}: {e}") from e
+        raise NativeError(f"cannot load {path}: {e}") from e
     P, I32, I64, S = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
     T = ctypes.POINTER(Tables)
     sig = {
@@ -102,7 +122,6 @@ def load():
     ver = lib.fcqt_abi_version()
     if ver != ABI_VERSION:
         raise NativeError(f"libflashcqt ABI {ver}, expected {ABI_VERSION}; rebuild")
-    _lib = lib
     return lib
 
 

@@ -31,6 +31,19 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), name
 
 
+def test_variant_library_exports_the_same_abi():
+    """The cross-lane variant library (same sources, band units of M <= 256
+    exchanging across lanes) loads with the library's C ABI: every declared
+    symbol and the same ABI version (no GPU call)."""
+    from flash_cqt import _native
+    xl = _native.load_variant("xlane")
+    for name in declared():
+        assert hasattr(xl, name), name
+    assert xl.fcqt_abi_version() == _native.ABI_VERSION
+    with pytest.raises(_native.NativeError):
+        _native.load_variant("nope")
+
+
 def test_abi_version(lib):
     from flash_cqt import _native
     assert lib.fcqt_abi_version() == _native.ABI_VERSION == 8
