@@ -52,6 +52,9 @@ struct SliceSrc {
     int S;
     long first;         // index in the signal of the call's slice 0
     long origin;        // signal sample index of sig[.][0]
+    int pairs;          // 1: every sample pair (jj even) is 8-byte aligned and wholly inside or
+                        // wholly outside the signal (even len and origin, 8-byte aligned sig and
+                        // win), so it is read with one 8-byte load (sliced_pair_vec)
 };
 
 constexpr int kQuarter = kN / 4;
@@ -66,6 +69,21 @@ __device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const float* 
     // fused multiply-adds): bitwise the windowed slice the reference framing
     // builds before its transform
     float p0 = src.win[jj] * a, p1 = src.win[jj + 1] * c;
+    asm volatile("" : "+v"(p0), "+v"(p1));
+    return make_float2(p0, p1);
+}
+
+// The same pair with src.pairs set: i = s0 + jj is even and len is even, so the
+// pair (i, i + 1) lies wholly inside [0, len) or wholly outside; one 8-byte
+// load at the clamped index (inside [0, len - 2], so in bounds) and one of the
+// window pair, zeros outside the signal. Same products as sliced_pair.
+__device__ __forceinline__ float2 sliced_pair_vec(const SliceSrc& src, const float* xrow, long s0, int sh, int n) {
+    const int jj = (2 * n + sh) & (kN - 1);
+    const long i = s0 + jj;
+    const bool in = i >= 0 && i <= src.len - 2;
+    const float2 x = *reinterpret_cast<const float2*>(xrow + min(max(i, 0l), src.len - 2));
+    const float2 w = *reinterpret_cast<const float2*>(src.win + jj);
+    float p0 = w.x * (in ? x.x : 0.0f), p1 = w.y * (in ? x.y : 0.0f);
     asm volatile("" : "+v"(p0), "+v"(p1));
     return make_float2(p0, p1);
 }
@@ -108,8 +126,13 @@ __device__ __forceinline__ void col_fwd_tile(const int b, const int cg, const fl
         const long g = src.first + sl;
         const long s0 = 2l * kQuarter * (g - 1) - src.origin;
         const int sh = (g & 1) ? kN - kQuarter : kQuarter;
+        if (src.pairs) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) v[r] = sliced_pair(src, xrow, s0, sh, 256 * (t + 8 * r) + n2);
+            for (int r = 0; r < 16; ++r) v[r] = sliced_pair_vec(src, xrow, s0, sh, 256 * (t + 8 * r) + n2);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = sliced_pair(src, xrow, s0, sh, 256 * (t + 8 * r) + n2);
+        }
     } else {
         const float2* xb = in + (long)b * kL;
 #pragma unroll

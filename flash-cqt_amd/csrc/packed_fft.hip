@@ -131,7 +131,7 @@ extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float
     return fwd_passes(reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
                       reinterpret_cast<float2*>(xs), reinterpret_cast<const float2*>(tab->tw_pass),
                       reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const float2*>(tab->tw_stage),
-                      SliceSrc{nullptr, nullptr, 1, 1, 0, 0}, false, batch, stream);
+                      SliceSrc{nullptr, nullptr, 1, 1, 0, 0, 0}, false, batch, stream);
 }
 
 extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float* f, float* y,
@@ -159,11 +159,13 @@ extern "C" int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int6
         !aligned(tab->tw_pass, 8) || !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
         return FCQT_EALIGN;
     const int64_t batch = nsig * nslices;
+    // pair loads when every sample pair is aligned and wholly inside or outside the signal
+    const int pairs = sig_len >= 2 && sig_len % 2 == 0 && origin % 2 == 0 && aligned(sig, 8) && aligned(window, 8);
     return fwd_passes(nullptr, reinterpret_cast<float2*>(work), reinterpret_cast<float2*>(xs),
                       reinterpret_cast<const float2*>(tab->tw_pass), reinterpret_cast<const float2*>(tab->tw_half),
                       reinterpret_cast<const float2*>(tab->tw_stage),
-                      SliceSrc{sig, window, (long)sig_len, (int)nslices, (long)first, (long)origin}, true, batch,
-                      stream);
+                      SliceSrc{sig, window, (long)sig_len, (int)nslices, (long)first, (long)origin, pairs}, true,
+                      batch, stream);
 }
 
 namespace fcqt {
@@ -189,6 +191,35 @@ __global__ __launch_bounds__(256) void k_overlap_add(const float* __restrict__ y
         }
     }
     out[(long)sig * length + p] = acc;
+}
+
+// The same sums four samples per thread (16-byte loads and stores), for an
+// output whose rows start 16-byte aligned (length % 4 == 0, aligned y and
+// out). p = 4 m: the four samples share the hop index, and jj..jj+3 stay
+// inside one slice row (jj is a multiple of 4 and N is too). Same additions
+// in the same order as k_overlap_add, so the same bits.
+__global__ __launch_bounds__(256) void k_overlap_add4(const float4* __restrict__ y, float4* __restrict__ out,
+                                                      int S, long length) {
+    const long p = 4 * ((long)blockIdx.x * 256 + threadIdx.x);
+    const int sig = blockIdx.y;
+    if (p >= length) return;
+    const long q = p + 2 * kQuarter;
+    const long sh = q / (2 * kQuarter);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const long s = sh - 1 + k;
+        if (s >= 0 && s < S) {
+            const int j = (int)(q - 2 * kQuarter * s);
+            const int jj = (j + ((s & 1) ? kQuarter : kN - kQuarter)) & (kN - 1);
+            const float4 v = y[(((long)sig * S + s) * kN + jj) / 4];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+    }
+    out[((long)sig * length + p) / 4] = acc;
 }
 }  // namespace fcqt
 
@@ -227,6 +258,12 @@ extern "C" int fcqt_overlap_add(const float* y, float* out, int64_t nsig, int64_
     if (!y || !out || nsig < 1 || nslices < 1 || length < 1 || nsig > 65535) return FCQT_EARG;
     if (nsig * nslices > kMaxBatch || length > nslices * 2 * (int64_t)kQuarter) return FCQT_EARG;
     if (!aligned(y, 4) || !aligned(out, 4)) return FCQT_EALIGN;
+    if (length % 4 == 0 && aligned(y, 16) && aligned(out, 16)) {
+        const dim3 grid4((unsigned)((length / 4 + 255) / 256), (unsigned)nsig);
+        hipLaunchKernelGGL(k_overlap_add4, grid4, dim3(256), 0, stream, reinterpret_cast<const float4*>(y),
+                           reinterpret_cast<float4*>(out), (int)nslices, (long)length);
+        return launch_status();
+    }
     const dim3 grid((unsigned)((length + 255) / 256), (unsigned)nsig);
     hipLaunchKernelGGL(k_overlap_add, grid, dim3(256), 0, stream, y, out, (int)nslices, (long)length);
     return launch_status();

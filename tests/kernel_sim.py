@@ -487,16 +487,20 @@ def scatter_bands(C, scat, tasks, ncoef):
 
 # ---------------------------------------------------------------- sliced framing
 
-def sliced_frames(sig, win, S, first=0, origin=0):
-    """The sliced column pass's read, index for index (sliced_pair in
-    packed_fft.hip): slice g = first + s of each signal row, sample j =
-    x[2H (g - 1) + jj] win[jj], jj = (j + H) mod N for even g and (j - H)
-    mod N for odd g, x[i] = sig[i - origin] inside the row and 0 outside.
+def sliced_frames(sig, win, S, first=0, origin=0, pairs=False):
+    """The sliced column pass's read, index for index (sliced_pair and, with
+    pairs=True, sliced_pair_vec in fcqt_passes.hpp): slice g = first + s of
+    each signal row, sample j = x[2H (g - 1) + jj] win[jj], jj = (j + H) mod N
+    for even g and (j - H) mod N for odd g, x[i] = sig[i - origin] inside the
+    row and 0 outside. The pair form reads samples (i, i + 1), i even, with
+    one load at i clamped to [0, len - 2]; it needs an even length and origin.
     Returns [nsig * S, N] float32 and asserts every clamped read in range."""
     H = N // 4
     nsig, length = sig.shape
     out = np.zeros((nsig * S, N), dtype=np.float32)
     j = np.arange(N)
+    if pairs:
+        assert length >= 2 and length % 2 == 0 and origin % 2 == 0
     for row in range(nsig):
         for s in range(S):
             g = first + s
@@ -504,10 +508,52 @@ def sliced_frames(sig, win, S, first=0, origin=0):
             sh = N - H if g & 1 else H
             jj = (j + sh) & (N - 1)
             i = s0 + jj
+            if pairs:
+                ie, je = i[0::2], jj[0::2]                 # pair starts: jj even
+                assert (ie % 2 == 0).all() and (je % 2 == 0).all() and (jj[1::2] == je + 1).all()
+                ic = np.clip(ie, 0, length - 2)
+                assert ic.min() >= 0 and ic.max() + 1 < length
+                inside = (ie >= 0) & (ie <= length - 2)
+                assert ((ie + 1 < length) == inside)[ie >= 0].all()   # pairs never straddle the end
+                a = np.where(inside, sig[row, ic], 0.0).astype(np.float32)
+                c = np.where(inside, sig[row, ic + 1], 0.0).astype(np.float32)
+                o = np.empty(N, np.float32)
+                o[0::2] = win[je] * a
+                o[1::2] = win[je + 1] * c
+                out[row * S + s] = o
+                continue
             ic = np.clip(i, 0, length - 1)
             assert ic.min() >= 0 and ic.max() < length
             a = sig[row, ic] * ((i >= 0) & (i < length)).astype(np.float32)
             out[row * S + s] = win[jj] * a
+    return out
+
+
+def overlap_add(y, nsig, S, length, vec4=False):
+    """k_overlap_add (one sample per thread) or k_overlap_add4 (four per
+    thread, length % 4 == 0): out[sig][p] = sum of the two slices covering
+    p + 2H, each read at its un-rolled index; asserts the four-sample reads
+    stay inside one slice row."""
+    H = N // 4
+    out = np.zeros((nsig, length), np.float32)
+    if vec4:
+        assert length % 4 == 0
+    for sig in range(nsig):
+        p = np.arange(0, length, 4) if vec4 else np.arange(length)
+        q = p + 2 * H
+        sh = q // (2 * H)
+        for k in range(2):
+            s = sh - 1 + k
+            ok = (s >= 0) & (s < S)
+            jv = q - 2 * H * s
+            jj = (jv + np.where(s & 1, H, N - H)) & (N - 1)
+            if vec4:
+                assert (jj % 4 == 0).all() and (jj[ok] + 3 < N).all()
+                for e in range(4):
+                    rows = (sig * S + s[ok]) * N + jj[ok] + e
+                    out[sig, p[ok] + e] += y.reshape(-1)[rows]
+            else:
+                out[sig, p[ok]] += y.reshape(-1)[(sig * S + s[ok]) * N + jj[ok]]
     return out
 
 

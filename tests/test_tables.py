@@ -202,6 +202,8 @@ def test_sliced_framing_index_math_cpu():
         ref = np.stack([np.roll(xp[:, 2 * H * s:2 * H * s + N] * win, -H if s % 2 == 0 else H, axis=1)
                         for s in range(S)], axis=1).reshape(2 * S, N)
         assert np.array_equal(ks.sliced_frames(x, win, S), ref)
+        if length % 2 == 0:          # the launcher's pair-load form
+            assert np.array_equal(ks.sliced_frames(x, win, S, pairs=True), ref)
         # streamed: chunks of hop samples, zero padded, one call per slice
         xs = np.concatenate([x, np.zeros((2, (S - 1) * hop - length), np.float32)], axis=1)
         chunks = [xs[:, i * hop:(i + 1) * hop] for i in range(S - 1)]
@@ -210,7 +212,28 @@ def test_sliced_framing_index_math_cpu():
             buf = np.concatenate([prev, chunk], axis=1)
             got = ks.sliced_frames(buf, win, 1, first=k, origin=hop * (k - 1))
             assert np.array_equal(got, ref.reshape(2, S, N)[:, k]), (length, k)
+            got = ks.sliced_frames(buf, win, 1, first=k, origin=hop * (k - 1), pairs=True)
+            assert np.array_equal(got, ref.reshape(2, S, N)[:, k]), (length, k)
             prev = chunk
+
+
+def test_overlap_add_index_math_cpu():
+    """Both overlap-add kernels' indexing (one sample per thread, and four
+    for lengths divisible by 4) equals the reference's roll of each inverse
+    slice by +H (even) / -H (odd), overlap-add at hop 2H and trim of 2H."""
+    N, H = ks.N, ks.N // 4
+    rs = np.random.RandomState(5)
+    for length in (8, 1000, 3 * 2 * H + 12, 5 * 2 * H):
+        quarters = -(-length // H)
+        S = (quarters + 1) // 2 + 1
+        y = rs.standard_normal((2 * S, N)).astype(np.float32)
+        full = np.zeros((2, (S + 1) * 2 * H), np.float32)
+        for s in range(S):
+            full[:, 2 * H * s:2 * H * s + N] += np.roll(y.reshape(2, S, N)[:, s], H if s % 2 == 0 else -H, axis=1)
+        ref = full[:, 2 * H:2 * H + length]
+        assert np.array_equal(ks.overlap_add(y, 2, S, length), ref)
+        if length % 4 == 0:
+            assert np.array_equal(ks.overlap_add(y, 2, S, length, vec4=True), ref)
 
 
 def test_stream_overlap_index_math_cpu():
