@@ -149,6 +149,25 @@ def test_analysis_batch_independent_bitwise(fused):
             assert torch.equal(torch.complex(kr1, ki1)[0], full[b])
 
 
+def test_every_batch_form_gives_the_same_bits(fused):
+    """Each batch size range runs other kernel forms: task-major band grids
+    with plain stores (B < 4) and with write-through stores (B = 4..63),
+    slice-major grids with write-through stores (B = 64..104) and with plain
+    stores, also in the wide inverse passes (B > 104); narrow pass tiles up to
+    B = 16. Rows of a B = 112 round trip (the last form) equal the B = 1, 8
+    and 64 results of the same rows bit for bit, coefficients and output."""
+    rs = np.random.RandomState(11)
+    x = gpu(rs.standard_normal((112, N)).astype(np.float32))
+    KR, KI = fused.fwd(x)
+    full = torch.complex(KR, KI).clone()
+    yfull = fused.bwd(KR, KI).clone()
+    for lo, B in ((0, 1), (37, 8), (40, 64)):
+        kr, ki = fused.fwd(x[lo:lo + B].contiguous())
+        assert torch.equal(torch.complex(kr, ki), full[lo:lo + B]), B
+        y = fused.bwd(kr, ki)
+        assert torch.equal(y, yfull[lo:lo + B]), B
+
+
 # ----------------------------------------------------------- synthesis
 
 def test_synthesis_matches_oracle(fused, oracle):
