@@ -168,6 +168,27 @@ def test_every_batch_form_gives_the_same_bits(fused):
         assert torch.equal(y, yfull[lo:lo + B]), B
 
 
+def test_adjoints_every_batch_form_same_bits(train):
+    """The two adjoints (analysis^H through the scatter engine with the
+    adjoint table, synthesis^H through the route engine with the dual-window
+    table) run the same batch-size forms: the input gradient of a B = 112
+    training step equals, row for row, the gradients of the same rows at
+    B = 1 and 8, bit for bit."""
+    rs = np.random.RandomState(12)
+    x = gpu(rs.standard_normal((112, N)).astype(np.float32))
+    t = gpu(rs.standard_normal((112, N)).astype(np.float32))
+
+    def grad(lo, B):
+        xg = x[lo:lo + B].clone().requires_grad_(True)
+        y = train.bwd(*train.fwd(xg))
+        ((y - t[lo:lo + B]) ** 2).sum().backward()
+        return xg.grad
+
+    full = grad(0, 112)
+    for lo, B in ((0, 1), (50, 8), (111, 1)):
+        assert torch.equal(grad(lo, B), full[lo:lo + B]), (lo, B)
+
+
 # ----------------------------------------------------------- synthesis
 
 def test_synthesis_matches_oracle(fused, oracle):
