@@ -74,6 +74,23 @@ extern "C" int fcqt_synthesis(const fcqt_tables* tab, const int32_t* scat, const
     return fcqt_packed_fft_inv(tab, ovf, f, y, work, batch, stream);
 }
 
+extern "C" int fcqt_stream_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
+                                     const int32_t* ovf, const float* coef, float* f, float* work, float* y,
+                                     float* tail, float* out, int64_t nsig, int64_t slice, hipStream_t stream) {
+    if (!scat || !groups || !ovf || !coef || !f || !work || !y || !tail) return FCQT_EARG;
+    if (slice > 0 && !out) return FCQT_EARG;
+    // every later step's arguments before the first launch
+    if (!tab || !tab->tw_pass || !tab->tw_half || nsig < 1 || nsig > 65535 || slice < 0 || slice > kMaxBatch)
+        return FCQT_EARG;
+    if (int e = check_band_args(tab, scat, coef, coef, FCQT_INTERLEAVED, nsig)) return e;
+    if (!aligned(f, 16) || !aligned(y, 8) || !aligned(work, 8) || !aligned(ovf, 4) || !aligned(groups, 16) ||
+        !aligned(tail, 4) || (out && !aligned(out, 4)))
+        return FCQT_EALIGN;
+    if (int e = fcqt_scatter_bands_sliced(tab, scat, groups, coef, f, nsig, 1, slice, stream)) return e;
+    if (int e = fcqt_packed_fft_inv(tab, ovf, f, y, work, nsig, stream)) return e;
+    return fcqt_stream_overlap(y, tail, out, nsig, slice, stream);
+}
+
 // ---------------------------------------------------------------------------
 // Allocation-free analysis. The spectrum X and the four-step intermediate W
 // of up to FCQT_STATIC_MAX_BATCH slices live in this file-scope device array

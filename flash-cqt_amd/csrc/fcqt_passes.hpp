@@ -46,25 +46,40 @@ __device__ __forceinline__ float2 dense_bin(const float2* __restrict__ fb, int i
 // origin = 2H (g - 1)). This is the zero padding, 50%-overlap unfold, Tukey
 // window and quarter roll of the reference SlicedCQT._slice in one read.
 struct SliceSrc {
-    const float* sig;   // [nsig][len]
+    const float* sig;   // [nsig][stride]: samples [0, split) of each row
     const float* win;   // [N]
-    long len;
+    long len;           // samples per row that the call holds
     int S;
     long first;         // index in the signal of the call's slice 0
-    long origin;        // signal sample index of sig[.][0]
+    long origin;        // signal sample index of sample 0 of the call's rows
     int pairs;          // 1: every sample pair (jj even) is 8-byte aligned and wholly inside or
-                        // wholly outside the signal (even len and origin, 8-byte aligned sig and
-                        // win), so it is read with one 8-byte load (sliced_pair_vec)
+                        // wholly outside the signal and on one side of split (even len, origin,
+                        // strides and split, 8-byte aligned buffers), so it is read with one 8-byte
+                        // load (sliced_pair_vec)
+    const float* sig2;  // [nsig][stride2]: samples [split, len) of each row (streamed slices:
+                        // the previous chunk in sig, the new chunk in sig2); null: sig holds all
+    long stride;        // floats between rows of sig
+    long stride2;       // floats between rows of sig2
+    long split;
+};
+
+// Row pointers of a sliced call: sample i of row sig is a[i] for i < split
+// and b[i - split] from split on.
+struct SliceRow {
+    const float* a;
+    const float* b;
+    long split;
+    __device__ __forceinline__ const float* at(long i) const { return i < split ? a + i : b + (i - split); }
 };
 
 constexpr int kQuarter = kN / 4;
 
-__device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const float* xrow, long s0, int sh, int n) {
+__device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const SliceRow& xrow, long s0, int sh, int n) {
     const int jj = (2 * n + sh) & (kN - 1);       // even: the pair (jj, jj + 1) stays inside the slice
     const long i = s0 + jj;
     const long i0 = min(max(i, 0l), src.len - 1), i1 = min(max(i + 1, 0l), src.len - 1);
-    const float a = xrow[i0] * ((i >= 0 && i < src.len) ? 1.0f : 0.0f);
-    const float c = xrow[i1] * ((i + 1 >= 0 && i + 1 < src.len) ? 1.0f : 0.0f);
+    const float a = *xrow.at(i0) * ((i >= 0 && i < src.len) ? 1.0f : 0.0f);
+    const float c = *xrow.at(i1) * ((i + 1 >= 0 && i + 1 < src.len) ? 1.0f : 0.0f);
     // rounded products (the empty asm keeps them out of the first butterfly's
     // fused multiply-adds): bitwise the windowed slice the reference framing
     // builds before its transform
@@ -74,14 +89,16 @@ __device__ __forceinline__ float2 sliced_pair(const SliceSrc& src, const float* 
 }
 
 // The same pair with src.pairs set: i = s0 + jj is even and len is even, so the
-// pair (i, i + 1) lies wholly inside [0, len) or wholly outside; one 8-byte
-// load at the clamped index (inside [0, len - 2], so in bounds) and one of the
-// window pair, zeros outside the signal. Same products as sliced_pair.
-__device__ __forceinline__ float2 sliced_pair_vec(const SliceSrc& src, const float* xrow, long s0, int sh, int n) {
+// pair (i, i + 1) lies wholly inside [0, len) or wholly outside, and (split
+// even) on one side of split; one 8-byte load at the clamped index (inside
+// [0, len - 2], so in bounds) and one of the window pair, zeros outside the
+// signal. Same products as sliced_pair.
+__device__ __forceinline__ float2 sliced_pair_vec(const SliceSrc& src, const SliceRow& xrow, long s0, int sh,
+                                                  int n) {
     const int jj = (2 * n + sh) & (kN - 1);
     const long i = s0 + jj;
     const bool in = i >= 0 && i <= src.len - 2;
-    const float2 x = *reinterpret_cast<const float2*>(xrow + min(max(i, 0l), src.len - 2));
+    const float2 x = *reinterpret_cast<const float2*>(xrow.at(min(max(i, 0l), src.len - 2)));
     const float2 w = *reinterpret_cast<const float2*>(src.win + jj);
     float p0 = w.x * (in ? x.x : 0.0f), p1 = w.y * (in ? x.y : 0.0f);
     asm volatile("" : "+v"(p0), "+v"(p1));
@@ -122,7 +139,9 @@ __device__ __forceinline__ void col_fwd_tile(const int b, const int cg, const fl
     if constexpr (SLICED) {
         const int sig = b / src.S;
         const int sl = b - sig * src.S;
-        const float* xrow = src.sig + (long)sig * src.len;
+        const SliceRow xrow{src.sig + (long)sig * src.stride,
+                            src.sig2 ? src.sig2 + (long)sig * src.stride2 : src.sig + (long)sig * src.stride + src.split,
+                            src.split};
         const long g = src.first + sl;
         const long s0 = 2l * kQuarter * (g - 1) - src.origin;
         const int sh = (g & 1) ? kN - kQuarter : kQuarter;

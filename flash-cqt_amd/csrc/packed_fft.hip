@@ -131,7 +131,7 @@ extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float
     return fwd_passes(reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(work),
                       reinterpret_cast<float2*>(xs), reinterpret_cast<const float2*>(tab->tw_pass),
                       reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const float2*>(tab->tw_stage),
-                      SliceSrc{nullptr, nullptr, 1, 1, 0, 0, 0}, false, batch, stream);
+                      SliceSrc{nullptr, nullptr, 1, 1, 0, 0, 0, nullptr, 1, 1, 1}, false, batch, stream);
 }
 
 extern "C" int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float* f, float* y,
@@ -164,8 +164,40 @@ extern "C" int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int6
     return fwd_passes(nullptr, reinterpret_cast<float2*>(work), reinterpret_cast<float2*>(xs),
                       reinterpret_cast<const float2*>(tab->tw_pass), reinterpret_cast<const float2*>(tab->tw_half),
                       reinterpret_cast<const float2*>(tab->tw_stage),
-                      SliceSrc{sig, window, (long)sig_len, (int)nslices, (long)first, (long)origin, pairs}, true,
-                      batch, stream);
+                      SliceSrc{sig, window, (long)sig_len, (int)nslices, (long)first, (long)origin, pairs, nullptr,
+                               (long)sig_len, (long)sig_len, (long)sig_len},
+                      true, batch, stream);
+}
+
+extern "C" int fcqt_stream_analysis(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
+                                    const float* prev, int64_t prev_stride, const float* next, int64_t next_stride,
+                                    const float* window, int64_t nsig, int64_t slice, float* coef, float* xs,
+                                    float* work, hipStream_t stream) {
+    constexpr long kHop = kN / 2;
+    if (!tab || !route || !groups || !prev || !next || !window || !coef || !xs || !work) return FCQT_EARG;
+    if (nsig < 1 || nsig > kMaxBatch || slice < 0 || slice > kMaxBatch) return FCQT_EARG;
+    if ((nsig > 1 && (prev_stride < kHop || next_stride < kHop)) || prev_stride < 0 || next_stride < 0 ||
+        prev_stride > ((int64_t)1 << 40) || next_stride > ((int64_t)1 << 40))
+        return FCQT_EARG;
+    // the band half first, so an argument error launches nothing
+    if (int e = check_band_args(tab, route, coef, coef, FCQT_INTERLEAVED, nsig)) return e;
+    if (!tab->tw_pass || !tab->tw_half) return FCQT_EARG;
+    if (!aligned(prev, 4) || !aligned(next, 4) || !aligned(window, 4) || !aligned(xs, 8) || !aligned(work, 8) ||
+        !aligned(groups, 16) || !aligned(tab->tw_pass, 8) || !aligned(tab->tw_half, 8))
+        return FCQT_EALIGN;
+    // slice `slice` of every signal is [prev row, next row]: the call holds
+    // the signal from sample hop (slice - 1) on, N samples per row, the first
+    // hop in prev and the rest in next
+    const int pairs = aligned(prev, 8) && aligned(next, 8) && aligned(window, 8) && prev_stride % 2 == 0 &&
+                      next_stride % 2 == 0;
+    if (int e = fwd_passes(nullptr, reinterpret_cast<float2*>(work), reinterpret_cast<float2*>(xs),
+                           reinterpret_cast<const float2*>(tab->tw_pass), reinterpret_cast<const float2*>(tab->tw_half),
+                           reinterpret_cast<const float2*>(tab->tw_stage),
+                           SliceSrc{prev, window, 2 * kHop, 1, (long)slice, kHop * ((long)slice - 1), pairs, next,
+                                    (long)prev_stride, (long)next_stride, kHop},
+                           true, nsig, stream))
+        return e;
+    return fcqt_route_bands_sliced(tab, route, groups, xs, coef, nsig, 1, slice, stream);
 }
 
 namespace fcqt {

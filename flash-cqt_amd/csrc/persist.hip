@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kFlowThreads) void k_flow_analysis(const FlowArgs p
     unsigned* rec = p.sync + (long)b * FCQT_SYNC_PER_SLICE;
     unsigned* err = p.sync + (long)p.batch * FCQT_SYNC_PER_SLICE;
     if (stage == 1) {
-        col_fwd_tile<false, kFColsPerTile>(b, t, p.x, p.work, p.twp, p.tws, SliceSrc{nullptr, nullptr, 1, 1, 0, 0, 0},
+        col_fwd_tile<false, kFColsPerTile>(b, t, p.x, p.work, p.twp, p.tws, SliceSrc{nullptr, nullptr, 1, 1, 0, 0, 0, nullptr, 1, 1, 1},
                                            lds);
         flow_signal(rec, kSyncStage1, true);
     } else if (stage == 2) {

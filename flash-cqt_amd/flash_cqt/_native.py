@@ -12,7 +12,7 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 SYNC_PER_SLICE = 64       # FCQT_SYNC_PER_SLICE: uint32 per slice in a single-launch counter buffer
 PLANAR = 0
 INTERLEAVED = 1
@@ -23,7 +23,8 @@ EXPORTS = ("fcqt_abi_version", "fcqt_status_string", "fcqt_last_hip_error",
            "fcqt_packed_fft_inv", "fcqt_analysis", "fcqt_synthesis", "fcqt_fill_zero",
            "fcqt_slice_fft_fwd", "fcqt_route_bands_sliced", "fcqt_scatter_bands_sliced",
            "fcqt_overlap_add", "fcqt_stream_overlap", "fcqt_image_check", "fcqt_tables_upload",
-           "fcqt_workspace_sizes", "fcqt_analysis_static", "fcqt_persist_analysis", "fcqt_persist_synthesis")
+           "fcqt_workspace_sizes", "fcqt_analysis_static", "fcqt_persist_analysis", "fcqt_persist_synthesis",
+           "fcqt_stream_analysis", "fcqt_stream_synthesis")
 
 
 class Tables(ctypes.Structure):
@@ -108,6 +109,8 @@ def _open(path):
         "fcqt_scatter_bands_sliced": ([T, P, P, P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_overlap_add": ([P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_stream_overlap": ([P, P, P, I64, I64, S], ctypes.c_int),
+        "fcqt_stream_analysis": ([T, P, P, P, I64, P, I64, P, I64, I64, P, P, P, S], ctypes.c_int),
+        "fcqt_stream_synthesis": ([T, P, P, P, P, P, P, P, P, P, I64, I64, S], ctypes.c_int),
         "fcqt_image_check": ([ctypes.c_char_p, I64, ctypes.POINTER(ImageInfo)], ctypes.c_int),
         "fcqt_tables_upload": ([ctypes.c_char_p, I64, P, I64, S, ctypes.POINTER(EngineTables)], ctypes.c_int),
         "fcqt_workspace_sizes": ([T, I64, ctypes.POINTER(Sizes)], ctypes.c_int),

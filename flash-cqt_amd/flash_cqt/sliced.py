@@ -19,7 +19,10 @@ fcqt_scatter_bands_sliced, fcqt_overlap_add): slices are read straight from
 the signal, coefficients are written and read in the block layout with the
 quarter roll applied, and the inverse slices are rolled and overlap-added
 in one pass. Blocks returned by that path are views of one buffer; passing
-them back to bwd reads that buffer without a copy.
+them back to bwd reads that buffer without a copy. The bounded-state stream
+(stream_fwd / stream_bwd) runs each step as one C-ABI call per direction
+(fcqt_stream_analysis reads the carried half slice and the new chunk in place,
+fcqt_stream_synthesis scatters, inverts and overlap-adds).
 """
 import math
 
@@ -342,19 +345,35 @@ class SlicedCQT:
             bufs["rows"]["captured"] = True      # recorded launches keep these addresses
         return st
 
+    @staticmethod
+    def _rows(t):
+        """A [B, C, n] chunk as nsig = B C fp32 rows with one row stride: the
+        tensor itself when it already is (e.g. a view into a longer signal),
+        else a contiguous fp32 copy. Returns (tensor, row stride in floats)."""
+        if t.dtype != torch.float32:
+            t = t.float()
+        B, C, n = t.shape
+        s0, s1, s2 = t.stride()
+        if s2 == 1:
+            if B * C == 1:
+                return t, n
+            rs = s0 if C == 1 else s1
+            if (B == 1 or s0 == C * s1) and rs >= n:
+                return t, rs
+        return t.contiguous(), n
+
     def _stream_slice_fused(self, f, prev, chunk, k):
         B, C, hop = chunk.shape
         nsig = B * C
-        buf = torch.cat([prev, chunk], dim=-1)         # [B, C, N]: the slice's samples
-        if buf.dtype != torch.float32:
-            buf = buf.float()
+        # the slice's samples are [prev row, chunk row]: one call reads both
+        # halves in place (no concatenated copy), frames, transforms and routes
+        pv, ps = self._rows(prev)
+        cv, cs = self._rows(chunk)
         st = self._stream_ptrs(f, nsig)
-        sh = _native.stream_handle(f.dev.index)
-        _native.check(f.lib.fcqt_slice_fft_fwd(f._ct, buf.data_ptr(), 2 * hop, st["tw"], nsig, 1, k, hop * (k - 1),
-                                               st["X"], st["W"], sh), "slice_fft_fwd")
         coef = torch.empty(nsig * f.ncoef, dtype=torch.complex64, device=f.dev)
-        _native.check(f.lib.fcqt_route_bands_sliced(f._ct, f._tp["route"], f._tp["slice_groups"], st["X"],
-                                                    coef.data_ptr(), nsig, 1, k, sh), "route_bands_sliced")
+        _native.check(f.lib.fcqt_stream_analysis(f._ct, f._tp["route"], f._tp["slice_groups"], pv.data_ptr(), ps,
+                                                 cv.data_ptr(), cs, st["tw"], nsig, k, coef.data_ptr(), st["X"],
+                                                 st["W"], _native.stream_handle(f.dev.index)), "stream_analysis")
         ng = len(self.oct_bins)
         views = [coef.as_strided((B, C, b, M), (C * b * M, b * M, M, 1), nsig * off) for b, M, off in f.gspec]
         return views[:ng], views[ng:]
@@ -404,16 +423,13 @@ class SlicedCQT:
                     tail = tail.to(device=f.dev, dtype=torch.float32).contiguous()
                 coef = self._block_buffer(f, blocks, side, nsig, 1)
                 st = self._stream_ptrs(f, nsig)
-                sh = _native.stream_handle(f.dev.index)
-                _native.check(f.lib.fcqt_scatter_bands_sliced(f._ct, f._tp["scat"], f._tp["slice_groups"],
-                                                              coef.data_ptr(), st["F"], nsig, 1, k, sh),
-                              "scatter_bands_sliced")
-                _native.check(f.lib.fcqt_packed_fft_inv(f._ct, f._tp["ovf_scat"], st["F"], st["Y"], st["W"], nsig,
-                                                        sh), "packed_fft_inv")
                 out = torch.empty(B, C, self.hop, dtype=torch.float32, device=f.dev) if k > 0 else None
-                _native.check(f.lib.fcqt_stream_overlap(st["Y"], tail.data_ptr(),
-                                                        out.data_ptr() if out is not None else None, nsig, k, sh),
-                              "stream_overlap")
+                # scatter, inverse passes and the half-slice overlap-add in one call
+                _native.check(f.lib.fcqt_stream_synthesis(f._ct, f._tp["scat"], f._tp["slice_groups"],
+                                                          f._tp["ovf_scat"], coef.data_ptr(), st["F"], st["W"],
+                                                          st["Y"], tail.data_ptr(),
+                                                          out.data_ptr() if out is not None else None, nsig, k,
+                                                          _native.stream_handle(f.dev.index)), "stream_synthesis")
                 if out is not None:
                     yield out
                 k += 1

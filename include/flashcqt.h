@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 8
+#define FCQT_ABI_VERSION 9
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -336,6 +336,37 @@ int fcqt_overlap_add(const float* y, float* out, int64_t nsig, int64_t nslices, 
  * (sliced.py:194-209). */
 int fcqt_stream_overlap(const float* y, float* tail, float* out, int64_t nsig, int64_t slice,
                         hipStream_t stream);
+
+/* One streamed analysis step: slice `slice` of each of nsig signals, whose
+ * 65536 samples are the row of prev (the previous hop of 32768 samples)
+ * followed by the row of next (the new hop), framed (window, quarter roll)
+ * and transformed as fcqt_slice_fft_fwd does with nslices = 1, first =
+ * slice, origin = 32768 (slice - 1) on the concatenated buffer, then routed
+ * into the sliced block layout as fcqt_route_bands_sliced with first = slice.
+ * The caller passes zeros as prev for slice 0 and as next for the final
+ * flush. No concatenated copy is made.
+ *   prev, next  nsig rows of 32768 fp32 each, rows prev_stride / next_stride
+ *               floats apart (>= 32768 when nsig > 1; a chunk that is a view
+ *               into a longer signal is read in place)
+ *   coef        nsig * ncoef complex (interleaved)
+ *   xs, work    as for fcqt_packed_fft_fwd with batch nsig
+ * Replaces the per-slice step of SlicedCQT.stream_fwd (sliced.py:171-192):
+ * the concatenation of the carried half slice with the new chunk, _slice,
+ * the pack copy, fft3, fwd_bands and _arrange. */
+int fcqt_stream_analysis(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
+                         const float* prev, int64_t prev_stride, const float* next, int64_t next_stride,
+                         const float* window, int64_t nsig, int64_t slice, float* coef, float* xs,
+                         float* work, hipStream_t stream);
+
+/* One streamed synthesis step: fcqt_scatter_bands_sliced (one slice per
+ * signal, first = slice), fcqt_packed_fft_inv and fcqt_stream_overlap in one
+ * call, with every argument checked before the first launch. out may be NULL
+ * for slice 0.
+ * Replaces the per-slice step of SlicedCQT.stream_bwd (sliced.py:194-209):
+ * _arrange, inv_bands, inv_tail, the roll and the half-slice overlap-add. */
+int fcqt_stream_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
+                          const int32_t* ovf, const float* coef, float* f, float* work, float* y,
+                          float* tail, float* out, int64_t nsig, int64_t slice, hipStream_t stream);
 
 /* Zero n floats with a fill kernel (graph-capture safe, no hipMemsetAsync). */
 int fcqt_fill_zero(float* buf, int64_t n, hipStream_t stream);

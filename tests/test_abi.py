@@ -46,7 +46,7 @@ def test_variant_library_exports_the_same_abi():
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 8
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 9
 
 
 def test_status_strings(lib):
@@ -94,6 +94,19 @@ def test_argument_errors_detected_before_any_launch(lib):
     assert lib.fcqt_stream_overlap(p, p, null, 1, 2, s) == EARG                 # output needed after slice 0
     assert lib.fcqt_stream_overlap(p, p, p, 0, 1, s) == EARG
     assert lib.fcqt_stream_overlap(p, p, p, 1, -1, s) == EARG
+    # streamed composites: (tab, route, groups, prev, prev_stride, next, next_stride, window, nsig, slice,
+    # coef, xs, work, stream) and (tab, scat, groups, ovf, coef, f, work, y, tail, out, nsig, slice, stream)
+    T = ctypes.byref(tab)
+    H2 = 32768
+    assert lib.fcqt_stream_analysis(T, p, p, null, H2, p, H2, p, 1, 0, p, p, p, s) == EARG      # no prev
+    assert lib.fcqt_stream_analysis(T, p, p, p, H2, p, H2, p, 0, 0, p, p, p, s) == EARG         # no signals
+    assert lib.fcqt_stream_analysis(T, p, p, p, H2, p, H2, p, 1, -1, p, p, p, s) == EARG        # negative slice
+    assert lib.fcqt_stream_analysis(T, p, p, p, 100, p, H2, p, 2, 0, p, p, p, s) == EARG        # rows overlap
+    assert lib.fcqt_stream_analysis(T, p, ctypes.c_void_p(4104), p, H2, p, H2, p, 1, 0, p, p, p, s) == EALIGN
+    assert lib.fcqt_stream_synthesis(T, p, p, p, p, p, p, p, null, p, 1, 1, s) == EARG   # no tail
+    assert lib.fcqt_stream_synthesis(T, p, p, p, p, p, p, p, p, null, 1, 2, s) == EARG   # output needed
+    assert lib.fcqt_stream_synthesis(T, p, p, p, p, p, p, p, p, p, 65536, 1, s) == EARG  # too many signals
+    assert lib.fcqt_stream_synthesis(T, p, p, p, p, odd, p, p, p, p, 1, 1, s) == EALIGN  # F alignment
     assert lib.fcqt_overlap_add(p, p, 1, 1, 2 * 32768 + 1, s) == EARG      # longer than nslices * 2H
     assert lib.fcqt_overlap_add(p, null, 1, 1, 10, s) == EARG
     assert lib.fcqt_fill_zero(p, 0, s) == 0  # nothing to do, no launch

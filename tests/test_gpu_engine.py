@@ -541,6 +541,37 @@ def test_sliced_stream_equals_whole_buffer():
     assert md < 1e-5 and rd < 1e-5
 
 
+def test_sliced_stream_chunk_layouts_same_bits():
+    """The streamed analysis reads the carried half slice and the new chunk
+    in place through row strides: chunks that are contiguous, views into a
+    longer [B, C, L] signal (one row stride), views whose rows have no single
+    stride (read from a contiguous copy) and float64 chunks (converted) give
+    the same coefficients and output bit for bit."""
+    from flash_cqt import SlicedCQT
+    s = SlicedCQT(device=_dev())
+    rs = np.random.RandomState(21)
+    L = 3 * s.hop
+    x = gpu(rs.standard_normal((2, 3, L)))
+    xt = x.transpose(0, 1).contiguous().transpose(0, 1)       # same values, rows without one stride
+    layouts = {
+        "contiguous": [x[..., i * s.hop:(i + 1) * s.hop].contiguous() for i in range(3)],
+        "views": [x[..., i * s.hop:(i + 1) * s.hop] for i in range(3)],
+        "no single stride": [xt[..., i * s.hop:(i + 1) * s.hop] for i in range(3)],
+        "float64": [x[..., i * s.hop:(i + 1) * s.hop].double() for i in range(3)],
+    }
+    res = {}
+    with torch.no_grad():
+        for name, chunks in layouts.items():
+            sl = list(s.stream_fwd(iter(chunks)))
+            coefs = [torch.cat([c.reshape(-1) for c in list(b) + list(sd)]) for b, sd in sl]
+            ys = torch.cat(list(s.stream_bwd(iter(sl))), dim=-1)
+            res[name] = (coefs, ys)
+    ref = res["contiguous"]
+    for name, (coefs, ys) in res.items():
+        assert all(torch.equal(a, b) for a, b in zip(coefs, ref[0])), name
+        assert torch.equal(ys, ref[1]), name
+
+
 def test_sliced_stream_fused_equals_host_framing():
     """Streaming with the framing in the kernels (one fused call per slice,
     the overlap-add carrying the tail) equals the host-framed stream bit for
