@@ -529,6 +529,41 @@ def sliced_frames(sig, win, S, first=0, origin=0, pairs=False):
     return out
 
 
+def stream_frames(prev, nxt, win, first, pairs=True):
+    """fcqt_stream_analysis's framing read: slice `first` of each row from
+    two buffers, samples [0, hop) of the slice in prev and [hop, N) in nxt
+    (SliceRow.at), s0 = 0 (origin = hop (first - 1)), with the pair loads of
+    sliced_pair_vec or the scalar reads of sliced_pair. Asserts that every
+    read stays inside its own buffer's row. Returns [nsig, N] float32."""
+    H = N // 4
+    hop = 2 * H
+    nsig = prev.shape[0]
+    assert prev.shape == nxt.shape == (nsig, hop)
+    j = np.arange(N)
+    sh = N - H if first & 1 else H
+    jj = (j + sh) & (N - 1)
+    out = np.zeros((nsig, N), np.float32)
+
+    def at(row, i):
+        i = np.asarray(i)
+        a = i < hop
+        assert (i[a] >= 0).all() and (i[a] < hop).all() and (i[~a] - hop >= 0).all() and (i[~a] - hop < hop).all()
+        return np.where(a, prev[row, np.clip(i, 0, hop - 1)], nxt[row, np.clip(i - hop, 0, hop - 1)])
+    for row in range(nsig):
+        i = jj                                   # s0 = 0: the slice is exactly [prev, nxt]
+        if pairs:
+            ie = i[0::2]
+            assert ((ie < hop) == (ie + 1 < hop)).all()        # a pair never straddles the split
+            ic = np.clip(ie, 0, N - 2)
+            o = np.empty(N, np.float32)
+            o[0::2] = win[jj[0::2]] * at(row, ic)
+            o[1::2] = win[jj[1::2]] * at(row, ic + 1)
+            out[row] = o
+        else:
+            out[row] = win[jj] * at(row, i)
+    return out
+
+
 def overlap_add(y, nsig, S, length, vec4=False):
     """k_overlap_add (one sample per thread) or k_overlap_add4 (four per
     thread, length % 4 == 0): out[sig][p] = sum of the two slices covering

@@ -214,6 +214,9 @@ def test_sliced_framing_index_math_cpu():
             assert np.array_equal(got, ref.reshape(2, S, N)[:, k]), (length, k)
             got = ks.sliced_frames(buf, win, 1, first=k, origin=hop * (k - 1), pairs=True)
             assert np.array_equal(got, ref.reshape(2, S, N)[:, k]), (length, k)
+            for pairs in (True, False):            # the two-buffer read of fcqt_stream_analysis
+                got = ks.stream_frames(prev, chunk, win, k, pairs=pairs)
+                assert np.array_equal(got, ref.reshape(2, S, N)[:, k]), (length, k, pairs)
             prev = chunk
 
 
