@@ -31,9 +31,9 @@ namespace fcqt {
 constexpr int kN = 65536;        // slice length (real samples)
 constexpr int kL = 32768;        // packed complex length N/2
 constexpr int kFStride = kL + 64;  // complex elements per half-spectrum plane (>= L + 1)
-constexpr int kOvfCap = 1024;      // overflow bins (more than two taps) per scatter table
+constexpr int kOvfCap = 4096;      // overflow bins (more than two taps) per scatter table
 constexpr int kFRow = 2 * kFStride + 2 * kOvfCap;  // complex elements per batch row of F
-constexpr int kFoldPerWg = 256;    // overflow fold-list entries per inverse column workgroup
+constexpr int kFoldPerWg = 512;    // overflow fold-list entries per inverse column workgroup
 constexpr int kXStride = kL + 64;  // complex elements per row of the rfft spectrum X (>= L + 1)
 
 // ------------------------------------------------------------ complex ops

@@ -36,7 +36,7 @@ Everything the kernels need that does not depend on the batch:
            of degree > 2. Every slot has one writer, the set of written slots
            is fixed by the table, and slots never written stay zero, so F
            needs zeroing only once.
-  ovf_*    per scatter table, int32 [8][256] fold lists for the inverse
+  ovf_*    per scatter table, int32 [8][512] fold lists for the inverse
            column pass: workgroup w (columns 16w..16w+15 and their mirrors)
            adds the overflow slots of the bins of degree > 2 in its columns;
            entry = bin | overflow index << 16, -1 = none.
@@ -60,11 +60,11 @@ import numpy as np
 N = 65536
 L = N // 2
 FSTRIDE = L + 64            # complex elements per half-spectrum plane (>= L + 1)
-OVF_CAP = 1024              # bins with more than two contributing taps, per table
+OVF_CAP = 4096              # bins with more than two contributing taps, per table
 FROW = 2 * FSTRIDE + 2 * OVF_CAP   # complex elements per batch row of F
 INV_COLS_PER_WG = 32        # inverse column pass: 16 columns + their 16 mirrors per workgroup
 INV_WGS = 256 // INV_COLS_PER_WG    # 8 inverse column workgroups per slice
-FOLD_PER_WG = 256           # fold-list entries per inverse column workgroup (one per thread)
+FOLD_PER_WG = 512           # fold-list entries per inverse column workgroup
 XSTRIDE = L + 64            # complex elements per row of the real-FFT spectrum X
 POINTS_PER_TASK = 2048      # 128 threads x 16 values per band workgroup
 STAGE_ORDER = ((16, 2), (16, 4), (16, 8), (16, 16), (256, 2), (256, 4), (256, 8))

@@ -39,14 +39,14 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 9
+#define FCQT_ABI_VERSION 10
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
 #define FCQT_FSTRIDE 32832    /* complex elements per half-spectrum plane (>= L+1) */
-#define FCQT_OVF_CAP 1024     /* overflow bins (more than two taps) per scatter table */
-#define FCQT_FROW 67712       /* complex elements per batch row of F: 2 slot planes of FCQT_FSTRIDE + 2 x FCQT_OVF_CAP */
-#define FCQT_OVF_LEN 2048     /* int32 entries of a scatter table's overflow fold lists [8][256] */
+#define FCQT_OVF_CAP 4096     /* overflow bins (more than two taps) per scatter table */
+#define FCQT_FROW 73856       /* complex elements per batch row of F: 2 slot planes of FCQT_FSTRIDE + 2 x FCQT_OVF_CAP */
+#define FCQT_OVF_LEN 4096     /* int32 entries of a scatter table's overflow fold lists [8][512] */
 #define FCQT_XSTRIDE 32832    /* complex elements per batch row of the real-FFT spectrum X (>= L+1) */
 #define FCQT_TW_STAGE_LEN 4064 /* complex elements of the stage twiddle table */
 #define FCQT_TW_PASS_LEN 32768 /* complex elements of the pass twiddle table [128][256] */

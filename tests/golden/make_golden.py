@@ -1,6 +1,8 @@
 """Write the golden fixtures that pin the oracle to the reference.
 
 Runs ONCE, in the build container, on CPU:  python tests/golden/make_golden.py
+(golden_ref.npz, the headline layout) and python tests/golden/make_golden.py
+layouts (golden_layouts.npz, four further layouts).
 
 Why an import: the reference holds no golden vectors, and the bank numerics
 (np.round ties in filterbank.py:129-149, the mirrored block-size write one
@@ -118,5 +120,67 @@ def main():
     print("wrote", OUT / "golden_ref.npz", (OUT / "golden_ref.npz").stat().st_size, "bytes")
 
 
+# Further layouts the reference's factored engine accepts (band lengths
+# 32-2048), chosen for what they stress: the most bins with three or four
+# taps found over ~1000 random layouts (more than 2048 overflow bins, ~300 in
+# one inverse column workgroup), four taps on one bin, two octave groups at
+# another rate, and an octave group of a single band.
+LAYOUTS = (
+    (([6, 2, 1], [4, 12, 24]), 16000),
+    (([2, 5, 2], [4, 8, 64]), 44100),
+    (([4, 3], [12, 48]), 48000),
+    (([1, 2, 2], [4, 16, 96]), 22050),
+)
+STRIDE_LAYOUTS = 13
+SLICED_LAYOUT = 1           # index into LAYOUTS of the layout also run sliced
+
+
+def layouts():
+    """golden_layouts.npz: for each of LAYOUTS, the group table hashes, the
+    block shapes, and forward / inverse vectors of the reference on the
+    closed-form inputs (first row only), plus one sliced run."""
+    sys.path.insert(0, str(REF))
+    from flash_cqt import OctCQT, SlicedCQT  # noqa: E402  (reference, CPU only)
+
+    torch.set_num_threads(8)
+    fx = {}
+    x, _ = inputs()
+    xt = torch.from_numpy(x[:1])
+    for li, ((octs, bpo), fs) in enumerate(LAYOUTS):
+        cqt = OctCQT(octs, bpo, fs=fs, audio_len=N, device="cpu")
+        groups = list(cqt.groups) + list(cqt.side_groups)
+        fx[f"l{li}_layout"] = np.array(octs + [-1] + bpo + [-1, fs], dtype=np.int64)
+        fx[f"l{li}_group_shapes"] = np.array([list(g[0].shape) for g in groups], dtype=np.int64)
+        fx[f"l{li}_group_table_sha256"] = np.array(
+            [[sha(idx.numpy().astype(np.int64)), sha(gv.numpy().astype(np.float32)),
+              sha(pos.numpy().astype(np.int64)), sha(gdv.numpy().astype(np.float32)),
+              sha(conj.numpy().astype(np.bool_))] for idx, gv, pos, gdv, conj in groups])
+        with torch.no_grad():
+            blocks, side = cqt.fwd(xt)
+            flat = torch.cat([c.reshape(1, -1) for c in list(blocks) + list(side)], dim=-1)
+            y = cqt.bwd(blocks, side)
+        fx[f"l{li}_fwd_sub"] = flat[:, ::STRIDE_LAYOUTS].numpy().astype(np.complex64)
+        fx[f"l{li}_bwd_sub"] = y[:, ::STRIDE_LAYOUTS].numpy().astype(np.float32)
+    (octs, bpo), fs = LAYOUTS[SLICED_LAYOUT]
+    s = SlicedCQT(octs, bpo, fs=fs, sl_len=N, device="cpu")
+    xs = torch.from_numpy(sliced_input()[:, :1])
+    with torch.no_grad():
+        sb, ss = s.fwd(xs)
+        ys_ = s.bwd(sb, ss, length=xs.shape[-1])
+    fx["sliced_shapes"] = np.array([list(c.shape) for c in sb], dtype=np.int64)
+    fx["sliced_blocks_sub"] = torch.cat(
+        [c.reshape(1, -1)[..., ::STRIDE_SLICED] for c in sb], dim=-1).numpy().astype(np.complex64)
+    fx["sliced_side_sub"] = torch.cat(
+        [c.reshape(1, -1)[..., ::STRIDE_LAYOUTS] for c in ss], dim=-1).numpy().astype(np.complex64)
+    fx["sliced_bwd_sub"] = ys_[..., ::STRIDE_LAYOUTS].numpy().astype(np.float32)
+    fx["meta_versions"] = np.array([torch.__version__, np.__version__])
+    fx["meta_stride"] = np.array([STRIDE_LAYOUTS, STRIDE_SLICED, SLICED_LAYOUT])
+    np.savez_compressed(OUT / "golden_layouts.npz", **fx)
+    print("wrote", OUT / "golden_layouts.npz", (OUT / "golden_layouts.npz").stat().st_size, "bytes")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["layouts"]:
+        layouts()
+    else:
+        main()

@@ -46,7 +46,24 @@ def test_variant_library_exports_the_same_abi():
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 9
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 10
+
+
+def test_header_constants_match_tables_and_kernels():
+    """The layout macros of flashcqt.h, the device constants of fcqt_fft.hpp
+    and the table builder's constants are one set of numbers."""
+    from flash_cqt import tables as T
+    h = dict(re.findall(r"#define (FCQT_[A-Z_]+) (\d+)", HEADER.read_text()))
+    k = dict(re.findall(r"constexpr int (k\w+) = ([^;]+);",
+                        (ROOT / "flash-cqt_amd" / "csrc" / "fcqt_fft.hpp").read_text()))
+    want = {"FCQT_N": T.N, "FCQT_L": T.L, "FCQT_FSTRIDE": T.FSTRIDE, "FCQT_OVF_CAP": T.OVF_CAP,
+            "FCQT_FROW": T.FROW, "FCQT_OVF_LEN": T.INV_WGS * T.FOLD_PER_WG, "FCQT_XSTRIDE": T.XSTRIDE,
+            "FCQT_TW_STAGE_LEN": T.TW_STAGE_LEN}
+    for name, v in want.items():
+        assert int(h[name]) == v, name
+    assert int(k["kOvfCap"]) == T.OVF_CAP and int(k["kFoldPerWg"]) == T.FOLD_PER_WG
+    assert k["kFRow"].replace(" ", "") == "2*kFStride+2*kOvfCap" and k["kFStride"].startswith("kL + ")
+    assert T.FROW % 32 == 0          # F rows stay 256-byte aligned
 
 
 def test_status_strings(lib):

@@ -1,0 +1,145 @@
+"""GPU parity of the HIP engine on four OctCQT layouts besides the headline
+[3,4,2]/[8,16,32] (the layouts of tests/golden/golden_layouts.npz, whose
+oracle tables test_layouts.py pins to the reference bit for bit).
+
+Same bars as the headline layout: forward coefficients >= 120 dB against the
+oracle (>= 115 dB per group), synthesis >= 120 dB, round trip >= 125 dB,
+both gradients >= 120 dB, and the sliced transform of one layout against
+the sliced oracle. Layout 0 fills more than half of the synthesis overflow
+area; layout 1 has bins with four taps."""
+import numpy as np
+import pytest
+import torch
+
+from golden.golden_inputs import inputs, cotangents, sliced_input
+from oracle import cqt_oracle as co
+
+pytestmark = pytest.mark.gpu
+
+N = 65536
+NLAYOUTS = 4
+
+
+def _dev():
+    return torch.device("cuda:0")
+
+
+def gpu(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(_dev())
+
+
+def cnp(t):
+    t = t.detach().cpu()
+    if t.is_complex():
+        return t.numpy().astype(np.complex128)
+    return t.numpy().astype(np.float64)
+
+
+@pytest.fixture(scope="module")
+def gl():
+    import pathlib
+    return np.load(pathlib.Path(__file__).resolve().parent / "golden" / "golden_layouts.npz",
+                   allow_pickle=False)
+
+
+def layout(gl, i):
+    v = gl[f"l{i}_layout"].tolist()
+    a = v.index(-1)
+    b = v.index(-1, a + 1)
+    return v[:a], v[a + 1:b], v[b + 1]
+
+
+_eng = {}
+
+
+def engines(gl, i):
+    """(oracle, FusedOctCQT, TrainableCQT) of layout i, built once."""
+    if i not in _eng:
+        from flash_cqt import OctCQT
+        from flash_cqt.fused import FusedOctCQT
+        from flash_cqt.trainable import TrainableCQT
+        octs, bpo, fs = layout(gl, i)
+        print(f"layout {i}: num_octs {octs} bins_per_oct {bpo} fs {fs}", flush=True)
+        c = OctCQT(octs, bpo, fs=fs, audio_len=N, device=_dev())
+        _eng[i] = (co.OctCQT(octs, bpo, fs, N), FusedOctCQT(c, _dev()), TrainableCQT(c, _dev()))
+    return _eng[i]
+
+
+@pytest.mark.parametrize("i", range(NLAYOUTS))
+def test_layout_analysis_synthesis_round_trip(gl, i):
+    o, f, _ = engines(gl, i)
+    assert f.ncoef == o.ncoef
+    x = np.concatenate([inputs()[0], np.random.RandomState(60 + i).standard_normal((1, N))]).astype(np.float32)
+    KR, KI = f.fwd(gpu(x))
+    got = cnp(KR) + 1j * cnp(KI)
+    ref = o.flatten(*o.fwd(x))
+    db = co.snr_db(ref, got)
+    print(f"layout {i}: analysis {db:.2f} dB", flush=True)
+    assert db >= 120
+    for b, M, off in f.gspec:
+        assert co.snr_db(ref[:, off:off + b * M], got[:, off:off + b * M]) >= 115, (b, M, off)
+    y = cnp(f.bwd(KR, KI))
+    assert co.snr_db(x, y) >= 125
+    C = ref.astype(np.complex64)
+    ys = cnp(f.bwd(gpu(C.real), gpu(C.imag)))
+    db = co.snr_db(o.bwd(*o.unflatten(C.astype(np.complex128))), ys)
+    print(f"layout {i}: synthesis {db:.2f} dB", flush=True)
+    assert db >= 120
+
+
+@pytest.mark.parametrize("i", range(NLAYOUTS))
+def test_layout_gradients(gl, i):
+    o, _, train = engines(gl, i)
+    x, u = inputs()
+    ys = cotangents(o.ncoef)
+    xg = gpu(x).requires_grad_(True)
+    bl, sd = train.fwd(xg)
+    flat = torch.cat([c.reshape(2, -1) for c in list(bl) + list(sd)], -1)
+    (torch.view_as_real(flat) * gpu(ys)).sum().backward()
+    G = ys[..., 0].astype(np.float64) + 1j * ys[..., 1]
+    db = co.snr_db(o.fwd_adjoint(*o.unflatten(G)), cnp(xg.grad))
+    print(f"layout {i}: analysis gradient {db:.2f} dB", flush=True)
+    assert db >= 120
+    C = o.flatten(*o.fwd(x)).astype(np.complex64)
+    blk, sid = o.unflatten(C)
+    leaves = [torch.from_numpy(np.ascontiguousarray(c)).to(_dev()).requires_grad_(True)
+              for c in list(blk) + list(sid)]
+    ng = len(o.groups)
+    (train.bwd(leaves[:ng], leaves[ng:]) * gpu(u)).sum().backward()
+    got = np.concatenate([cnp(lv.grad).reshape(2, -1) for lv in leaves], -1)
+    db = co.snr_db(o.flatten(*o.bwd_adjoint(u)), got)
+    print(f"layout {i}: synthesis gradient {db:.2f} dB", flush=True)
+    assert db >= 120
+
+
+def test_layout_sliced_matches_oracle(gl):
+    """SlicedCQT of the fixture's sliced layout on the HIP engine (framing in
+    the kernels) against the sliced oracle, and its stream equal to the whole
+    buffer."""
+    from flash_cqt import SlicedCQT
+    i = int(gl["meta_stride"][2])
+    octs, bpo, fs = layout(gl, i)
+    s = SlicedCQT(octs, bpo, fs=fs, device=_dev())
+    assert type(s.cqt).__name__ == "TrainableCQT"
+    x = sliced_input()
+    with torch.no_grad():
+        bl, sd = s.fwd(gpu(x))
+        y = s.bwd(bl, sd, length=x.shape[-1])
+    so = co.SlicedCQT(octs, bpo, fs)
+    obl, osd = so.fwd(x)
+    got = np.concatenate([cnp(c).reshape(-1) for c in list(bl) + list(sd)])
+    ref = np.concatenate([c.reshape(-1) for c in list(obl) + list(osd)])
+    assert co.snr_db(ref, got) >= 120
+    assert co.snr_db(so.bwd(obl, osd, length=x.shape[-1]), cnp(y)) >= 120
+    assert co.snr_db(x, cnp(y)) >= 125
+    xs = gpu(x[:, :1, :98304])
+    with torch.no_grad():
+        bw, sw = s.fwd(xs)
+        chunks = [xs[..., k * s.hop:(k + 1) * s.hop] for k in range(xs.shape[-1] // s.hop)]
+        out = list(s.stream_fwd(iter(chunks)))
+        ystr = torch.cat(list(s.stream_bwd(iter(out))), dim=-1)[..., :xs.shape[-1]]
+        yw = s.bwd(bw, sw, length=xs.shape[-1])
+    m = s.size_per_oct
+    md = max(float((c - bw[j][..., k * m[j]:(k + 1) * m[j]]).abs().max())
+             for k, (blk, _) in enumerate(out) for j, c in enumerate(blk))
+    assert md < 1e-5 and float((ystr - yw).abs().max()) < 1e-5

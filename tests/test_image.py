@@ -63,6 +63,7 @@ def _patched(image, sid, index, value, dtype=np.int32):
 
 def test_corrupted_images_are_refused(lib, image, factored_tables):
     """Each corruption names a bound a kernel relies on."""
+    from flash_cqt import tables as T
     t = factored_tables
     nt = t["tasks"].shape[0]
     bad = {}
@@ -94,10 +95,10 @@ def test_corrupted_images_are_refused(lib, image, factored_tables):
     bad["route bin"] = _patched(image, 5, 2 * 777, 32769)
     bad["route bin with a high bit"] = _patched(image, 5, 2 * 778, np.int32(np.uint32(5 | (1 << 31)).view(np.int32)))
     bad["adjoint route bin"] = _patched(image, 6, 2 * 1234, 40000)
-    bad["scatter slot"] = _patched(image, 7, 2 * 99, 2 * 32832 + 2 * 1024)
+    bad["scatter slot"] = _patched(image, 7, 2 * 99, T.FROW)
     bad["scatter mode"] = _patched(image, 8, 2 * 5, np.int32(np.uint32(3 << 30).view(np.int32)))
     bad["fold bin"] = _patched(image, 9, 0, 32769)
-    bad["fold index"] = _patched(image, 10, 1, 5 | (1024 << 16))
+    bad["fold index"] = _patched(image, 10, 1, 5 | (T.OVF_CAP << 16))
     bad["slice roll"] = _patched(image, 11, 2, 2)
     bad["slice group past ncoef"] = _patched(image, 11, 4 * (nt - 1) + 1, 10 ** 6)
     for name, img in bad.items():
