@@ -57,6 +57,13 @@ class FusedOctCQT:
 
     def __init__(self, cqt, device=None):
         assert cqt.nn == N, "fused path is built for sl_len 65536"
+        groups = _np_groups(cqt)
+        bad = sorted({g[0].shape[1] for g in groups} - set(T.BAND_LENGTHS))
+        if bad:
+            # the reference's factored engine has no stages for them either
+            # (fused.py:274-299: roots rmr[::M // 32], radix factors up to 2048)
+            raise ValueError(f"band lengths {bad} of this layout are outside the engine's "
+                             f"{T.BAND_LENGTHS[0]}..{T.BAND_LENGTHS[-1]}")
         dev = torch.device(device) if device is not None else torch.device(cqt.device)
         if dev.type != "cuda":
             raise ValueError("FusedOctCQT runs on a GPU (device 'cuda')")
@@ -66,7 +73,7 @@ class FusedOctCQT:
         self.cqt = cqt
         self.lib = _native.load()
 
-        built = T.build(_np_groups(cqt), noct=len(cqt.groups))
+        built = T.build(groups, noct=len(cqt.groups))
         self.gspec = built["gspec"]
         self.ncoef = built["ncoef"]
         # the tables go to the device as one table image through the C ABI's

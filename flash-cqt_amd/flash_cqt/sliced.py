@@ -9,8 +9,8 @@ octave coefficients are rolled back by a quarter of each block.
 
 The per-slice engine is any object with fwd(x[..., sl_len]) -> (blocks, side)
 and bwd(blocks, side) -> x. engine="auto" uses the fused HIP engine
-(TrainableCQT, differentiable) on a GPU device with sl_len 65536 and the
-pure-torch OctCQT otherwise; "hip" forces the fused engine, "torch" the
+(TrainableCQT, differentiable) for fp32 on a GPU device with sl_len 65536 and
+band lengths 32..2048, and the pure-torch OctCQT otherwise; "hip" forces the fused engine, "torch" the
 pure-torch one. Assigning self.cqt swaps engines as in the reference.
 
 With the HIP engine and no gradient to record, fwd and bwd run the framing
@@ -68,14 +68,10 @@ class SlicedCQT:
         self.oct_bins = oct_.oct_bins
         self.size_per_oct = oct_.size_per_oct
         self.frqs_hz = oct_.frqs_hz
-        # 'auto' takes the fp32 HIP engine only for fp32 on a GPU at the fused
-        # slice length; other dtypes keep the torch engine (which computes in
-        # the requested precision, as the reference's OctCQT does)
-        use_hip = engine == "hip" or (engine == "auto" and self.device.type == "cuda"
-                                      and sl_len == 65536 and dtype == torch.float32)
         if engine not in ("auto", "hip", "torch"):
             raise ValueError("engine must be 'auto', 'hip' or 'torch'")
-        if use_hip:
+        lengths = {g[0].shape[1] for g in oct_.np_groups + oct_.np_side_groups}
+        if engine == "hip" or (engine == "auto" and self.auto_picks_hip(self.device, sl_len, dtype, lengths)):
             from .trainable import TrainableCQT
             self.cqt = TrainableCQT(oct_, device)
         else:
@@ -84,6 +80,17 @@ class SlicedCQT:
         # run the framing inside the HIP engine's kernels when it can (False:
         # always frame on the host around self.cqt, as the reference does)
         self.fused_framing = True
+
+    @staticmethod
+    def auto_picks_hip(device, sl_len, dtype, lengths):
+        """engine='auto' takes the fp32 HIP engine for fp32 on a GPU at the
+        fused slice length when every band length is one the engine runs
+        (32..2048, as the reference's factored engine); otherwise the torch
+        engine, which computes in the requested precision and takes any
+        layout, as the reference's OctCQT does."""
+        from .tables import BAND_LENGTHS
+        return (torch.device(device).type == "cuda" and sl_len == 65536 and dtype == torch.float32
+                and all(M in BAND_LENGTHS for M in lengths))
 
     # ------------------------------------------------------------ latency
 

@@ -143,3 +143,26 @@ def test_layout_sliced_matches_oracle(gl):
     md = max(float((c - bw[j][..., k * m[j]:(k + 1) * m[j]]).abs().max())
              for k, (blk, _) in enumerate(out) for j, c in enumerate(blk))
     assert md < 1e-5 and float((ystr - yw).abs().max()) < 1e-5
+
+
+def test_layout_outside_the_engine_keeps_the_torch_engine():
+    """A layout with band length 16 ([3,3,3] / [16,32,64]) on the GPU:
+    FusedOctCQT refuses it, and SlicedCQT's 'auto' runs it on the torch
+    engine (torch.fft, the reference's own OctCQT path) at the oracle's
+    values."""
+    from flash_cqt import OctCQT, SlicedCQT
+    from flash_cqt.fused import FusedOctCQT
+    with pytest.raises(ValueError, match="band lengths"):
+        FusedOctCQT(OctCQT([3, 3, 3], [16, 32, 64], fs=44100, audio_len=N, device=_dev()), _dev())
+    s = SlicedCQT([3, 3, 3], [16, 32, 64], fs=44100, device=_dev())
+    assert type(s.cqt).__name__ == "OctCQT"
+    x = sliced_input()[:, :1]
+    with torch.no_grad():
+        bl, sd = s.fwd(gpu(x))
+        y = s.bwd(bl, sd, length=x.shape[-1])
+    so = co.SlicedCQT([3, 3, 3], [16, 32, 64], 44100)
+    obl, _ = so.fwd(x)
+    got = np.concatenate([cnp(c).reshape(-1) for c in bl])
+    ref = np.concatenate([c.reshape(-1) for c in obl])
+    assert co.snr_db(ref, got) >= 120
+    assert co.snr_db(x, cnp(y)) >= 125

@@ -140,3 +140,29 @@ def test_layout_schedule_sim(gl, i):
     u = rs.standard_normal((1, N))
     gC = ks.route_bands(ks.packed_fft_fwd(u), t["route_b_taps"], t["bands"], t["tasks"], t["ncoef"])
     assert co.snr_db(o.flatten(*o.bwd_adjoint(u)), gC) > 140
+
+
+def test_unsupported_band_lengths_refused_and_auto_engine():
+    """A layout with a band length outside 32..2048 (here 16: [3,3,3] /
+    [16,32,64]) is refused by FusedOctCQT with a ValueError naming it, before
+    any device work, as the reference's factored engine cannot build it
+    either; SlicedCQT's 'auto' then keeps the torch engine, which takes any
+    layout (float64 and other slice lengths likewise)."""
+    import torch
+    from flash_cqt import OctCQT, SlicedCQT
+    from flash_cqt.fused import FusedOctCQT
+    c = OctCQT([3, 3, 3], [16, 32, 64], fs=44100, audio_len=N, device="cpu")
+    lengths = {g[0].shape[1] for g in c.np_groups + c.np_side_groups}
+    assert min(lengths) < 32
+    with pytest.raises(ValueError, match="band lengths"):
+        FusedOctCQT(c, "cuda")
+    pick = SlicedCQT.auto_picks_hip
+    ok = {32, 64, 2048}
+    assert pick("cuda", N, torch.float32, ok)
+    assert pick("cuda:0", N, torch.float32, ok)
+    assert not pick("cuda", N, torch.float32, lengths)
+    assert not pick("cuda", N, torch.float64, ok)
+    assert not pick("cpu", N, torch.float32, ok)
+    assert not pick("cuda", N // 2, torch.float32, ok)
+    s = SlicedCQT([3, 3, 3], [16, 32, 64], fs=44100, device="cpu")
+    assert type(s.cqt).__name__ == "OctCQT"
