@@ -112,6 +112,20 @@ def test_layout_gradients(gl, i):
     assert db >= 120
 
 
+@pytest.mark.parametrize("i", range(NLAYOUTS))
+def test_layout_single_launch_equals_six_launch(gl, i):
+    """The single-launch directions (persist_fwd / persist_inv) on this
+    layout's task table give the six-launch results bit for bit."""
+    _, f, _ = engines(gl, i)
+    x = gpu(np.random.RandomState(70 + i).standard_normal((3, N)))
+    KR, KI = f.fwd(x)
+    kr, ki, y = KR.clone(), KI.clone(), f.bwd(KR, KI).clone()
+    PR, PI = f.persist_fwd(x)
+    assert torch.equal(PR, kr) and torch.equal(PI, ki)
+    assert torch.equal(f.persist_inv(kr, ki), y)
+    assert f.sync_error(3) == 0
+
+
 def test_layout_sliced_matches_oracle(gl):
     """SlicedCQT of the fixture's sliced layout on the HIP engine (framing in
     the kernels) against the sliced oracle, and its stream equal to the whole
