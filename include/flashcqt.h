@@ -211,7 +211,7 @@ int fcqt_scatter_bands(const fcqt_tables* tab, const int32_t* scat /* [ntasks * 
  * is the sum of its scatter slots (imaginary parts of bins 0 and 32768
  * ignored, as irfft does). F is read only.
  *   ovf  [FCQT_OVF_LEN] int32 overflow fold lists of the scatter table that
- *        filled F: for each of the 8 column workgroups, up to 256 entries
+ *        filled F: for each of the 8 column workgroups, up to 512 entries
  *        bin | overflow index << 16 (-1 = none)
  *   f    [batch][FCQT_FROW] complex
  *   y    [batch][65536] fp32 out (8-byte aligned)
