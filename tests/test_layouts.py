@@ -17,6 +17,7 @@ import pytest
 import kernel_sim as ks
 from golden.golden_inputs import inputs, sliced_input
 from oracle import cqt_oracle as co
+from sweep_layouts import SWEEP
 
 N = 65536
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden" / "golden_layouts.npz"
@@ -166,3 +167,23 @@ def test_unsupported_band_lengths_refused_and_auto_engine():
     assert not pick("cuda", N // 2, torch.float32, ok)
     s = SlicedCQT([3, 3, 3], [16, 32, 64], fs=44100, device="cpu")
     assert type(s.cqt).__name__ == "OctCQT"
+
+
+@pytest.mark.parametrize("i", range(len(SWEEP)))
+def test_sweep_layout_schedule_sim(i):
+    """Index-math replay of the analysis and the synthesis (wide and narrow
+    inverse tiles) on the tables of a sweep layout, against the oracle."""
+    from flash_cqt import OctCQT, tables
+    octs, bpo, fs = SWEEP[i]
+    c = OctCQT(octs, bpo, fs=fs, audio_len=N, device="cpu")
+    t = tables.build(c.np_groups + c.np_side_groups)
+    o = co.OctCQT(octs, bpo, fs, N)
+    x = inputs()[0][1:].astype(np.float64)
+    C = ks.route_bands(ks.packed_fft_fwd(x), t["route_taps"], t["bands"], t["tasks"], t["ncoef"])
+    obl, osd = o.fwd(x)
+    Cref = o.flatten(obl, osd)
+    assert co.snr_db(Cref, C) > 140
+    F = ks.scatter_bands(Cref, t["scat_taps"], t["tasks"], t["ncoef"])
+    ref = o.bwd(obl, osd)
+    assert co.snr_db(ref, ks.packed_fft_inv(F, t["ovf_scat"], ks.WIDE)) > 140
+    assert co.snr_db(ref, ks.packed_fft_inv(F, t["ovf_scat"], ks.NARROW)) > 140
