@@ -14,6 +14,11 @@ namespace fcqt {
 // kernel has the most workgroups per slice (< 256), so this is generous.
 constexpr int64_t kMaxBatch = 1 << 22;
 
+// fcqt_analysis runs batches of kAnalysisChunkMinBatch slices and more in
+// chunks of kAnalysisChunk (the measurements are at the loop in abi.hip)
+constexpr int64_t kAnalysisChunk = 128;
+constexpr int64_t kAnalysisChunkMinBatch = 256;
+
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 // Checks shared by the band launchers (FCQT_OK, FCQT_EARG or FCQT_EALIGN):

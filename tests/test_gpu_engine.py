@@ -189,6 +189,36 @@ def test_adjoints_every_batch_form_same_bits(train):
         assert torch.equal(grad(lo, B), full[lo:lo + B]), (lo, B)
 
 
+def test_chunked_analysis_same_bits(fused, train):
+    """From 256 slices on, fcqt_analysis runs in chunks of 128 slices. A
+    B = 300 analysis (chunks of 128, 128 and 44), in both coefficient
+    layouts, and the synthesis adjoint of a B = 300 step (the analysis
+    engine with the dual-window table) equal the B = 1 results of rows on
+    both sides of each chunk edge bit for bit."""
+    rs = np.random.RandomState(13)
+    x = gpu(rs.standard_normal((300, N)).astype(np.float32))
+    KR, KI = fused.fwd(x)
+    full = torch.complex(KR, KI).clone()
+    with torch.no_grad():
+        bl, sd = train.fwd(x)
+        inter = torch.cat([c.reshape(300, -1) for c in list(bl) + list(sd)], -1)
+    rows = (0, 127, 128, 255, 256, 299)
+    for r in rows:
+        kr, ki = fused.fwd(x[r:r + 1].contiguous())
+        one = torch.complex(kr, ki)[0]
+        assert torch.equal(one, full[r]), r
+        assert torch.equal(one, inter[r]), r
+    u = gpu(rs.standard_normal((300, N)).astype(np.float32))
+    leaves = [c.detach().clone().requires_grad_(True) for c in list(bl) + list(sd)]
+    ng = len(bl)
+    (train.bwd(leaves[:ng], leaves[ng:]) * u).sum().backward()
+    g = torch.cat([lv.grad.reshape(300, -1) for lv in leaves], -1)
+    for r in rows:
+        l1 = [c[r:r + 1].detach().clone().requires_grad_(True) for c in list(bl) + list(sd)]
+        (train.bwd(l1[:ng], l1[ng:]) * u[r:r + 1]).sum().backward()
+        assert torch.equal(torch.cat([lv.grad.reshape(1, -1) for lv in l1], -1)[0], g[r]), r
+
+
 # ----------------------------------------------------------- synthesis
 
 def test_synthesis_matches_oracle(fused, oracle):
