@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kBandThreads) void k_route_bands(const float2* __re
     __shared__ float2 lds[kBandTaskLds];
     int task_id, b;
     decode_task<false, SM>(batch, ntasks, task_id, b);
-    route_task<LAYOUT, WT>(task_id, b, xs, cre, cim, rec, tasks, batch, ncoef, sm, tws, lds);
+    route_task<LAYOUT, WT>(task_id, b, xs, cre, cim, rec, tasks, ncoef, sm, tws, lds);
 }
 
 template <int LAYOUT, bool WT, bool SM>
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kBandThreads) void k_scatter_bands(const float* __r
     __shared__ float2 lds[kBandTaskLds];
     int task_id, b;
     decode_task<true, SM>(batch, ntasks, task_id, b);
-    scatter_task<LAYOUT, WT>(task_id, b, cre, cim, f, scat, tasks, batch, ncoef, sm, tws, lds);
+    scatter_task<LAYOUT, WT>(task_id, b, cre, cim, f, scat, tasks, ncoef, sm, tws, lds);
 }
 
 // From this batch size on the band kernels write their outputs through the
@@ -197,9 +197,53 @@ extern "C" int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* ro
     if (!aligned(xs, 8) || !aligned(groups, 16)) return FCQT_EALIGN;
     launch_route<kSliced>(tab->ntasks, batch, stream, reinterpret_cast<const float2*>(xs), coef, coef,
                           reinterpret_cast<const int2*>(route), reinterpret_cast<const int4*>(tab->tasks),
-                          (long)tab->ncoef, SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices, (int)first},
+                          (long)tab->ncoef,
+                          SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices, (int)first, (long)batch,
+                                   (int)nslices, 0, 0},
                           reinterpret_cast<const float2*>(tab->tw_stage));
     return launch_status();
+}
+
+extern "C" int fcqt_sliced_analysis(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
+                                    const float* sig, int64_t sig_len, const float* window, int64_t nsig,
+                                    int64_t nslices, float* coef, float* xs, float* work, hipStream_t stream) {
+    if (!sig || !window || !xs || !work || !groups || sig_len < 1) return FCQT_EARG;
+    if (nsig < 1 || nslices < 1 || nsig > kMaxBatch || nslices > kMaxBatch || nsig * nslices > kMaxBatch)
+        return FCQT_EARG;
+    const int64_t batch = nsig * nslices;
+    // the band half first, so an argument error launches nothing (the first
+    // chunk's framing pass checks the rest before its launch)
+    if (int e = check_band_args(tab, route, coef, coef, FCQT_INTERLEAVED, batch)) return e;
+    if (!aligned(xs, 8) || !aligned(groups, 16)) return FCQT_EALIGN;
+    // From kAnalysisChunkMinBatch slices on, chunks of about kAnalysisChunk
+    // slices (all signals of a range of slices, or ranges of signals one
+    // slice each), each framed, transformed and routed in turn so that its
+    // W and X are still in the memory-side cache when read (as fcqt_analysis
+    // does); a chunk's slices land in the whole call's block layout. The
+    // chunks reuse the leading rows of xs and work. Every slice gives the
+    // same bits however the call is cut.
+    int64_t ns = nsig, cs = nslices;
+    if (batch >= kAnalysisChunkMinBatch) {
+        ns = nsig < kAnalysisChunk ? nsig : kAnalysisChunk;
+        cs = kAnalysisChunk / ns;
+        cs = cs < 1 ? 1 : (cs > nslices ? nslices : cs);
+    }
+    const auto* g4 = reinterpret_cast<const int4*>(groups);
+    for (int64_t a = 0; a < nsig; a += ns) {
+        const int64_t na = nsig - a < ns ? nsig - a : ns;
+        for (int64_t c = 0; c < nslices; c += cs) {
+            const int64_t nc = nslices - c < cs ? nslices - c : cs;
+            if (int e = fcqt_slice_fft_fwd(tab, sig + a * sig_len, sig_len, window, na, nc, c, 0, xs, work, stream))
+                return e;
+            launch_route<kSliced>(tab->ntasks, na * nc, stream, reinterpret_cast<const float2*>(xs), coef, coef,
+                                  reinterpret_cast<const int2*>(route), reinterpret_cast<const int4*>(tab->tasks),
+                                  (long)tab->ncoef,
+                                  SliceMap{g4, (int)nc, (int)c, (long)batch, (int)nslices, (int)c, (int)a},
+                                  reinterpret_cast<const float2*>(tab->tw_stage));
+            if (int e = launch_status()) return e;
+        }
+    }
+    return FCQT_OK;
 }
 
 extern "C" int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
@@ -213,7 +257,8 @@ extern "C" int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* 
     if (!aligned(f, 16) || !aligned(groups, 16)) return FCQT_EALIGN;
     launch_scatter<kSliced>(tab->ntasks, batch, stream, coef, coef, f, reinterpret_cast<const int2*>(scat),
                             reinterpret_cast<const int4*>(tab->tasks), (long)tab->ncoef,
-                            SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices, (int)first},
+                            SliceMap{reinterpret_cast<const int4*>(groups), (int)nslices, (int)first, (long)batch,
+                                     (int)nslices, 0, 0},
                             reinterpret_cast<const float2*>(tab->tw_stage));
     return launch_status();
 }

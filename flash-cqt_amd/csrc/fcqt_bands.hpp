@@ -33,34 +33,41 @@ constexpr int kBandLds = cmax(cmax(cmax(band_lds(32), band_lds(64)), cmax(band_l
                               cmax(cmax(band_lds(512), band_lds(1024)), band_lds(2048)));
 
 // Coefficient addressing. FCQT_PLANAR / FCQT_INTERLEAVED: the engine layout
-// [batch][ncoef]. kSliced: the SlicedCQT block layout, interleaved complex:
-// batch = nsig * S slices (slice s of signal sig is batch row sig * S + s);
-// the coefficients of group g (first coefficient off_g, bins_g bands of
-// length M) form the block [nsig][bins_g][S * M] at batch * off_g, band i's
-// slice s at ((sig bins_g + i) S + s) M, and in octave groups (roll flag)
-// output m of the band transform sits at (m + M/4) mod M in even slices and
-// (m - M/4) mod M in odd slices (the SlicedCQT quarter roll; side groups are
-// [nsig][S][1][M] blocks, unrolled). Parity is that of the slice's index in
-// its signal, first + s, where first is the index of the call's first slice
-// (0 for a whole signal; the slice count so far when streaming).
+// [batch][ncoef]. kSliced: the SlicedCQT block layout, interleaved complex.
+// The call's batch = nsig * S slices (slice s of signal sig is batch row
+// sig * S + s) land in a block layout of NSIG signals x S_out slices
+// (rows = NSIG S_out) as its signal sig0 + sig, slice s0 + s: the
+// coefficients of group g (first coefficient off_g, bins_g bands of length
+// M) form the block [NSIG][bins_g][S_out * M] at rows * off_g, band i's
+// slice s at (((sig0 + sig) bins_g + i) S_out + s0 + s) M, and in octave
+// groups (roll flag) output m of the band transform sits at (m + M/4) mod M
+// in even slices and (m - M/4) mod M in odd slices (the SlicedCQT quarter
+// roll; side groups are [NSIG][S_out][1][M] blocks, unrolled). Parity is
+// that of the slice's index in its signal, first + s, where first is the
+// index of the call's first slice (0 for a whole signal; the chunk's first
+// slice; the slice count so far when streaming, with S_out = 1, s0 = 0).
 constexpr int kSliced = 2;
 
 struct SliceMap {
     const int4* __restrict__ groups;   // per task {off_g, bins_g, roll, 0}
     int S;                             // slices per signal in this call
     int first;                         // index in the signal of the call's slice 0
+    long rows;                         // rows of the block layout (NSIG * S_out)
+    int S_out;                         // slices per signal in the block layout
+    int s0;                            // layout slice of the call's slice 0
+    int sig0;                          // layout signal of the call's signal 0
 };
 
 template <int M, int LAYOUT>
 __device__ __forceinline__ void unit_coef(const int4 task, const int task_id, const int b, const int u,
-                                          const int batch, const long ncoef, const SliceMap& sm, long& base,
+                                          const long ncoef, const SliceMap& sm, long& base,
                                           int& shift) {
     if constexpr (LAYOUT == kSliced) {
         const int4 g = sm.groups[task_id];
         const int sig = b / sm.S;
         const int s = b - sig * sm.S;
         const int i = (task.y - g.x) / M + u;
-        base = (long)batch * g.x + ((long)(sig * g.y + i) * sm.S + s) * M;
+        base = sm.rows * g.x + ((long)((sm.sig0 + sig) * g.y + i) * sm.S_out + sm.s0 + s) * M;
         shift = g.z ? (((sm.first + s) & 1) ? M - M / 4 : M / 4) : 0;
     } else {
         base = (long)b * ncoef + task.y + u * M;
@@ -96,7 +103,7 @@ __device__ __forceinline__ void load_records(int2* rv, const int2* __restrict__ 
 // stored). The twiddle loads issue before the gathers, so their latency
 // hides under the record and gather round trips.
 template <int M, int LAYOUT, bool WT>
-__device__ __forceinline__ void route_band(const int4 task, const int task_id, const int b, const int batch,
+__device__ __forceinline__ void route_band(const int4 task, const int task_id, const int b,
                                            const int2* rv, const float2* __restrict__ xb,
                                            float* __restrict__ cre, float* __restrict__ cim,
                                            const long ncoef, const SliceMap sm,
@@ -123,7 +130,7 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
     if (u < task.z) {
         long ob;
         int shift;
-        unit_coef<M, LAYOUT>(task, task_id, b, u, batch, ncoef, sm, ob, shift);   // uniform per unit
+        unit_coef<M, LAYOUT>(task, task_id, b, u, ncoef, sm, ob, shift);   // uniform per unit
         float* orow = cre + (LAYOUT == FCQT_PLANAR ? ob : 2 * ob);
         float* oim = cim + (LAYOUT == FCQT_PLANAR ? ob : 0);
 #pragma unroll
@@ -136,7 +143,7 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
 }
 
 template <int M, int LAYOUT, bool WT>
-__device__ __forceinline__ void scatter_band(const int4 task, const int task_id, const int b, const int batch,
+__device__ __forceinline__ void scatter_band(const int4 task, const int task_id, const int b,
                                              const int2* __restrict__ scat, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
                                              const long ncoef, const SliceMap sm,
@@ -149,7 +156,7 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
     // after the transform)
     long ib;
     int shift;
-    unit_coef<M, LAYOUT>(task, task_id, b, active ? u : 0, batch, ncoef, sm, ib, shift);
+    unit_coef<M, LAYOUT>(task, task_id, b, active ? u : 0, ncoef, sm, ib, shift);
     const float* cr = cre + (LAYOUT == FCQT_PLANAR ? ib : 2 * ib);
     const float* ci = cim + (LAYOUT == FCQT_PLANAR ? ib : 0);
     float2 v[16];
@@ -202,7 +209,7 @@ template <int LAYOUT, bool WT = false>
 __device__ __forceinline__ void route_task(const int task_id, const int b, const float2* __restrict__ xs,
                                            float* __restrict__ cre, float* __restrict__ cim,
                                            const int2* __restrict__ rec, const int4* __restrict__ tasks,
-                                           const int batch, const long ncoef, const SliceMap& sm,
+                                           const long ncoef, const SliceMap& sm,
                                            const float2* __restrict__ tws, float2* lds) {
     float2* tw2 = lds + kBandLds;
     // the records issue first (they need the task index only); the task
@@ -212,7 +219,7 @@ __device__ __forceinline__ void route_task(const int task_id, const int b, const
     const float2* xb = xs + (long)b * kXStride;
     const int4 td = tasks[task_id];
     if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
-#define FCQT_ROUTE(M_) route_band<M_, LAYOUT, WT>(td, task_id, b, batch, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2)
+#define FCQT_ROUTE(M_) route_band<M_, LAYOUT, WT>(td, task_id, b, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
         case 32: FCQT_ROUTE(32); break;
         case 64: FCQT_ROUTE(64); break;
@@ -233,12 +240,12 @@ template <int LAYOUT, bool WT = false>
 __device__ __forceinline__ void scatter_task(const int task_id, const int b, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
                                              const int2* __restrict__ scat, const int4* __restrict__ tasks,
-                                             const int batch, const long ncoef, const SliceMap& sm,
+                                             const long ncoef, const SliceMap& sm,
                                              const float2* __restrict__ tws, float2* lds) {
     float2* tw2 = lds + kBandLds;
     const int4 td = tasks[task_id];
     if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
-#define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT, WT>(td, task_id, b, batch, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
+#define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT, WT>(td, task_id, b, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
     switch (td.x) {
         case 32: FCQT_SCATTER(32); break;
         case 64: FCQT_SCATTER(64); break;

@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kFlowThreads) void k_flow_analysis(const FlowArgs p
         flow_signal(rec, kSyncStage2, false);
     } else {
         flow_wait(rec, kSyncStage2, kFRowTiles, err);
-        route_task<LAYOUT, true>(t, b, p.xs, p.cre, p.cim, p.rec, p.tasks, p.batch, p.ncoef, SliceMap{nullptr, 1, 0},
+        route_task<LAYOUT, true>(t, b, p.xs, p.cre, p.cim, p.rec, p.tasks, p.ncoef, SliceMap{nullptr, 1, 0},
                                  p.tws, lds);
         flow_finish(rec, (unsigned)p.ntasks);
     }
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(kFlowThreads) void k_flow_synthesis(const FlowArgs 
     unsigned* rec = p.sync + (long)b * FCQT_SYNC_PER_SLICE;
     unsigned* err = p.sync + (long)p.batch * FCQT_SYNC_PER_SLICE;
     if (stage == 1) {
-        scatter_task<LAYOUT, false>(t, b, p.cre, p.cim, p.f, p.rec, p.tasks, p.batch, p.ncoef,
+        scatter_task<LAYOUT, false>(t, b, p.cre, p.cim, p.f, p.rec, p.tasks, p.ncoef,
                                     SliceMap{nullptr, 1, 0}, p.tws, lds);
         flow_signal(rec, kSyncStage1, true);
     } else if (stage == 2) {

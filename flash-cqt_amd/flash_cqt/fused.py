@@ -289,6 +289,25 @@ class FusedOctCQT:
                                                        _native.ptr(coef), nsig, nslices, first,
                                                        _native.stream_handle(self.dev.index)), "route_bands_sliced")
 
+    def sliced_analysis(self, sig, window, nslices, coef, xs, work, table="route"):
+        """slice_fft then route_bands_sliced of whole signals sig [nsig, len]
+        in one call (fcqt_sliced_analysis: from 256 slices on in chunks of
+        about 128 slices, same bits)."""
+        if sig.dim() != 2 or sig.shape[1] < 1:
+            raise ValueError("sig must be [nsig, len]")
+        nsig, length = sig.shape
+        self._need(sig, nsig * length * 4, "sig")
+        self._need(window, N * 4, "window")
+        B = nsig * nslices
+        self._need(xs, B * T.XSTRIDE * 8, "xs")
+        self._need(work, B * L * 8, "work")
+        self._need(coef, B * self.ncoef * 8, "coef")
+        _native.check(self.lib.fcqt_sliced_analysis(self._ct, _native.ptr(self.tables[table]),
+                                                    _native.ptr(self.tables["slice_groups"]), _native.ptr(sig), length,
+                                                    _native.ptr(window), nsig, nslices, _native.ptr(coef),
+                                                    _native.ptr(xs), _native.ptr(work),
+                                                    _native.stream_handle(self.dev.index)), "sliced_analysis")
+
     def scatter_bands_sliced(self, coef, f, nsig, nslices, table="scat", first=0):
         B = nsig * nslices
         self._need(coef, B * self.ncoef * 8, "coef")

@@ -14,7 +14,8 @@ band lengths 32..2048, and the pure-torch OctCQT otherwise; "hip" forces the fus
 pure-torch one. Assigning self.cqt swaps engines as in the reference.
 
 With the HIP engine and no gradient to record, fwd and bwd run the framing
-inside the engine's kernels (fcqt_slice_fft_fwd, fcqt_route_bands_sliced,
+inside the engine's kernels (fcqt_sliced_analysis, which frames, transforms
+and routes, in chunks of about 128 slices from 256 slices on;
 fcqt_scatter_bands_sliced, fcqt_overlap_add): slices are read straight from
 the signal, coefficients are written and read in the block layout with the
 quarter roll applied, and the inverse slices are rolled and overlap-added
@@ -250,9 +251,8 @@ class SlicedCQT:
         nsig = B * C
         sig = x.reshape(nsig, L).to(torch.float32).contiguous()
         ws = self._ws(f, nsig, S)
-        f.slice_fft(sig, self._tw32(), S, ws["X"], ws["W"])
         coef = torch.empty(nsig * S * f.ncoef, dtype=torch.complex64, device=f.dev)
-        f.route_bands_sliced(ws["X"], coef, nsig, S)
+        f.sliced_analysis(sig, self._tw32(), S, coef, ws["X"], ws["W"])
         ng = len(self.oct_bins)
         blocks, side = [], []
         for gi, (b, M, off) in enumerate(f.gspec):

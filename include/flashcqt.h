@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 10
+#define FCQT_ABI_VERSION 11
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -310,6 +310,22 @@ int fcqt_slice_fft_fwd(const fcqt_tables* tab, const float* sig, int64_t sig_len
 int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
                             const float* xs, float* coef, int64_t nsig, int64_t nslices, int64_t first,
                             hipStream_t stream);
+
+/* The whole-signal sliced analysis in one call: fcqt_slice_fft_fwd (first = 0,
+ * origin = 0) then fcqt_route_bands_sliced (first = 0), same arguments and
+ * the same block layout and bits. From 256 slices on it runs in chunks of
+ * about 128 slices (a range of slices of every signal, or a range of
+ * signals), each framed, transformed and routed before the next, so that a
+ * chunk's intermediates are still in the memory-side cache when read (xs
+ * and work then serve one chunk at a time, in their leading 128 rows).
+ *   sig    [nsig][sig_len] fp32,  window [65536] fp32
+ *   coef   nsig * nslices * ncoef complex (interleaved)
+ *   xs, work as for fcqt_packed_fft_fwd with batch nsig * nslices
+ * Replaces SlicedCQT.fwd's _slice, fwd_bands, _arrange and block permute
+ * (sliced.py:106-146) for a whole signal. */
+int fcqt_sliced_analysis(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
+                         const float* sig, int64_t sig_len, const float* window, int64_t nsig,
+                         int64_t nslices, float* coef, float* xs, float* work, hipStream_t stream);
 
 /* Band DFTs + slot scatter reading the same block layout (the inverse
  * arrange). F rules as fcqt_scatter_bands, batch nsig * nslices.

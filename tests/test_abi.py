@@ -46,7 +46,7 @@ def test_variant_library_exports_the_same_abi():
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 10
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 11
 
 
 def test_header_constants_match_tables_and_kernels():
@@ -124,6 +124,13 @@ def test_argument_errors_detected_before_any_launch(lib):
     assert lib.fcqt_stream_synthesis(T, p, p, p, p, p, p, p, p, null, 1, 2, s) == EARG   # output needed
     assert lib.fcqt_stream_synthesis(T, p, p, p, p, p, p, p, p, p, 65536, 1, s) == EARG  # too many signals
     assert lib.fcqt_stream_synthesis(T, p, p, p, p, odd, p, p, p, p, 1, 1, s) == EALIGN  # F alignment
+    # whole-signal sliced analysis: (tab, route, groups, sig, sig_len, window, nsig, nslices, coef, xs, work, stream)
+    assert lib.fcqt_sliced_analysis(T, p, p, null, 100, p, 1, 1, p, p, p, s) == EARG           # no signal
+    assert lib.fcqt_sliced_analysis(T, p, p, p, 0, p, 1, 1, p, p, p, s) == EARG                # empty signal
+    assert lib.fcqt_sliced_analysis(T, p, p, p, 100, p, 1, 0, p, p, p, s) == EARG              # no slices
+    assert lib.fcqt_sliced_analysis(T, p, p, p, 100, p, 1 << 12, 1 << 12, p, p, p, s) == EARG  # too many rows
+    assert lib.fcqt_sliced_analysis(T, p, p, p, 100, p, 1, 1, p, p, null, s) == EARG           # no work buffer
+    assert lib.fcqt_sliced_analysis(T, p, ctypes.c_void_p(4104), p, 100, p, 1, 1, p, p, p, s) == EALIGN
     assert lib.fcqt_overlap_add(p, p, 1, 1, 2 * 32768 + 1, s) == EARG      # longer than nslices * 2H
     assert lib.fcqt_overlap_add(p, null, 1, 1, 10, s) == EARG
     assert lib.fcqt_fill_zero(p, 0, s) == 0  # nothing to do, no launch
@@ -146,6 +153,7 @@ def test_coefficient_span_beyond_ncoef_is_refused(lib):
         assert lib.fcqt_scatter_bands_sliced(tab, p, p, p, p, 1, 1, 0, s) == 1
         assert lib.fcqt_analysis(tab, p, p, p, p, 0, p, p, 1, s) == 1
         assert lib.fcqt_synthesis(tab, p, p, p, p, 0, p, p, p, 1, s) == 1
+        assert lib.fcqt_sliced_analysis(tab, p, p, p, 100, p, 1, 1, p, p, p, s) == 1
 
 
 def test_static_analysis_argument_errors_before_any_launch(lib):

@@ -706,6 +706,34 @@ def test_sliced_fused_framing_equals_engine_composition():
     assert torch.equal(y3, y4.detach())
 
 
+@pytest.mark.parametrize("nsig,S", [(1, 300), (3, 100), (300, 2), (2, 128)])
+def test_sliced_chunked_analysis_same_bits(fused, nsig, S):
+    """fcqt_sliced_analysis cuts calls of 256 slices and more into chunks
+    (slice ranges of every signal: 1 x 300 -> 128 + 128 + 44, 3 x 100 -> 42
+    slices per chunk; signal ranges: 300 x 2 -> 128 + 128 + 44 signals, one
+    slice each); the block buffer equals the unchunked framing pass + route
+    (fcqt_slice_fft_fwd, fcqt_route_bands_sliced) bit for bit, and below 256
+    slices (2 x 128) the composite is those two calls."""
+    rs = np.random.RandomState(17)
+    hop = N // 2
+    length = (S - 2) * hop + 777 if S > 2 else 20000
+    sig = gpu(rs.standard_normal((nsig, length)).astype(np.float32))
+    from flash_cqt.sliced import makewnd
+    win = makewnd(N, N // 4, device=_dev()).float().contiguous()
+    from flash_cqt import SlicedCQT
+    assert SlicedCQT()._num_slices(length) == S
+    B = nsig * S
+    xs = torch.empty(B, 32832, 2, device=_dev())
+    work = torch.empty(B, 32768, 2, device=_dev())
+    ref = torch.empty(B * fused.ncoef, dtype=torch.complex64, device=_dev())
+    fused.slice_fft(sig, win, S, xs, work)
+    fused.route_bands_sliced(xs, ref, nsig, S)
+    got = torch.full_like(ref, float("nan"))
+    fused.sliced_analysis(sig, win, S, got, xs, work)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("length", [1, 1000, 16384, 32768, 32769, 65536, 131071, 262144])
 def test_sliced_fused_ragged_lengths(length):
     """Short, hop-aligned and ragged signal lengths, two channels: the fused
