@@ -222,7 +222,10 @@ int fcqt_packed_fft_inv(const fcqt_tables* tab, const int32_t* ovf, const float*
                         float* work, int64_t batch, hipStream_t stream);
 
 /* Analysis in one call: fcqt_packed_fft_fwd then fcqt_route_bands.
- * xs is [batch][FCQT_XSTRIDE] and work [batch][32768] complex scratch. */
+ * xs is [batch][FCQT_XSTRIDE] and work [batch][32768] complex scratch. From
+ * 256 slices on the call runs the three kernels chunk by chunk, 128 slices
+ * at a time, so that each chunk's intermediates are still in the
+ * memory-side cache when read; the results are the same bits. */
 int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                   float* coef_re, float* coef_im, int layout,
                   float* xs, float* work, int64_t batch, hipStream_t stream);
