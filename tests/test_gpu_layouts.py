@@ -219,3 +219,41 @@ def test_sweep_layout_parity(i):
     (torch.view_as_real(flat) * gpu(ys_)).sum().backward()
     G = ys_[..., 0].astype(np.float64) + 1j * ys_[..., 1]
     assert co.snr_db(o.fwd_adjoint(*o.unflatten(G)), cnp(xg.grad)) >= 120
+
+
+@pytest.mark.parametrize("i", [2, 5, 8])
+def test_sweep_layout_sliced(i):
+    """SlicedCQT on sweep layouts (fused framing): blocks and side bands
+    >= 120 dB against the sliced oracle, round trip within 1 dB of the
+    reference algorithm's fp32 reconstruction or >= 125 dB, and the bounded
+    stream equal to the whole buffer."""
+    from flash_cqt import SlicedCQT
+    octs, bpo, fs = SWEEP[i]
+    s = SlicedCQT(octs, bpo, fs=fs, device=_dev())
+    assert type(s.cqt).__name__ == "TrainableCQT"
+    x = sliced_input()[:, :1]
+    with torch.no_grad():
+        bl, sd = s.fwd(gpu(x))
+        y = s.bwd(bl, sd, length=x.shape[-1])
+    so = co.SlicedCQT(octs, bpo, fs)
+    obl, osd = so.fwd(x)
+    got = np.concatenate([cnp(c).reshape(-1) for c in list(bl) + list(sd)])
+    ref = np.concatenate([c.reshape(-1) for c in list(obl) + list(osd)])
+    assert co.snr_db(ref, got) >= 120
+    rt = co.snr_db(x, cnp(y))
+    with torch.no_grad():
+        st = SlicedCQT(octs, bpo, fs=fs, device=_dev(), engine="torch")
+        lib_rt = co.snr_db(x, cnp(st.bwd(*st.fwd(gpu(x)), length=x.shape[-1])))
+    print(f"sweep {i} sliced: round trip {rt:.2f} dB, torch.fft fp32 {lib_rt:.2f} dB", flush=True)
+    assert rt >= min(125.0, lib_rt - 1.0)
+    xs = gpu(x[..., :98304])
+    with torch.no_grad():
+        bw, sw = s.fwd(xs)
+        chunks = [xs[..., k * s.hop:(k + 1) * s.hop] for k in range(xs.shape[-1] // s.hop)]
+        out = list(s.stream_fwd(iter(chunks)))
+        ystr = torch.cat(list(s.stream_bwd(iter(out))), dim=-1)[..., :xs.shape[-1]]
+        yw = s.bwd(bw, sw, length=xs.shape[-1])
+    m = s.size_per_oct
+    md = max(float((c - bw[j][..., k * m[j]:(k + 1) * m[j]]).abs().max())
+             for k, (blk, _) in enumerate(out) for j, c in enumerate(blk))
+    assert md < 1e-5 and float((ystr - yw).abs().max()) < 1e-5
