@@ -437,4 +437,55 @@ __device__ __forceinline__ void row_inv_tile(const int b, const int rg, const fl
     }
 }
 
+// The inverse row pass of one slice s of a SlicedCQT signal with the
+// overlap-add in its store (whole-signal synthesis; orow is the signal's
+// output row of `length` samples). Slice s's samples jj, jj + 1 (jj =
+// 2 (kk1 + 128 k2)) go to p, p + 1 with p = 2H (s - 1) + j, j = (jj + H)
+// mod N in even slices and (jj - H) mod N in odd ones, where p < length.
+// Even slices (one launch) store 0 + v; odd slices (the next launch) add v
+// to that, or store 0 + v in their second half when there is no slice
+// s + 1. The values are the rounded products k_row_inv stores, so the sums
+// are k_overlap_add's (0 + a) + b up to the order of two operands, which
+// gives the same bits. PAIR: length even and orow 8-byte aligned, so p and
+// p + 1 are both in range or both out, and one 8-byte access serves both.
+template <int RPW, bool ODD, bool PAIR>
+__device__ __forceinline__ void row_inv_ola_tile(const int b, const int rg, const int s, const int S,
+                                                 const long length, const float2* __restrict__ in,
+                                                 float* __restrict__ orow, const float2* __restrict__ tws,
+                                                 float2* lds) {
+    using P = Plan<256>;
+    float2* tw2 = lds + RPW * P::US;
+    const int rho = threadIdx.x >> 4;
+    const int t = threadIdx.x & 15;
+    row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * RPW + rho) * 256, lds, tw2, rho, t, 16 * RPW, tws,
+                          nullptr, nullptr);
+    const int rho2 = threadIdx.x & (RPW - 1);
+    const int kg = threadIdx.x / RPW;
+    const float2* s2 = lds + rho2 * P::US;
+    const int kk1 = rg * RPW + rho2;
+    constexpr float sc = 0.5f / (float)kL;     // 1/L of the inverse, 1/2 of the retangle
+    const long base = 2l * kQuarter * (s - 1);
+    const bool last = s + 1 >= S;              // no slice s + 1
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int k2 = kg + 16 * u;
+        const float2 w = s2[pad16(k2)];
+        const int j = (2 * (kk1 + 128 * k2) + (ODD ? kN - kQuarter : kQuarter)) & (kN - 1);
+        const long p = base + j;
+        float v0 = w.x * sc, v1 = -w.y * sc;
+        asm volatile("" : "+v"(v0), "+v"(v1));    // the rounded products, as k_row_inv stores them
+        const bool add = ODD && (j < 2 * kQuarter || !last);
+        if constexpr (PAIR) {
+            if (p >= 0 && p < length) {
+                float2* o = reinterpret_cast<float2*>(orow + p);
+                const float2 a = add ? *o : make_float2(0.0f, 0.0f);
+                *o = make_float2(a.x + v0, a.y + v1);
+            }
+        } else {
+            if (p >= 0 && p < length) orow[p] = (add ? orow[p] : 0.0f) + v0;
+            if (p + 1 >= 0 && p + 1 < length) orow[p + 1] = (add ? orow[p + 1] : 0.0f) + v1;
+        }
+    }
+}
+
 }  // namespace fcqt

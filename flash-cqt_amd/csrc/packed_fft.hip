@@ -117,9 +117,85 @@ static int inv_passes(const float2* f, float2* work, float2* y, const float2* tw
     return launch_inv_passes<kInvColsWide, kRowsWide, false>(f, work, y, twp, twh, ovf, tws, batch, stream);
 }
 
+// The inverse row pass with the sliced overlap-add in its store
+// (row_inv_ola_tile): the slices of one parity of nsig signals x S slices,
+// nper of them per signal; work row sig * S + s, output row sig of `length`.
+template <int RPW, bool ODD, bool PAIR>
+__global__ __launch_bounds__(16 * RPW) void k_row_inv_ola(const float2* __restrict__ in, float* __restrict__ out,
+                                                          const float2* __restrict__ tws, int S, long length,
+                                                          int nper) {
+    constexpr int kWgs = 128 / RPW;               // workgroups per slice
+    __shared__ float2 lds[row_lds<RPW>()];
+    const int lg = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int r = lg / kWgs;                      // sig * nper + m: slice s = 2 m + ODD of signal sig
+    const int sig = r / nper;
+    const int s = 2 * (r - sig * nper) + (ODD ? 1 : 0);
+    row_inv_ola_tile<RPW, ODD, PAIR>(sig * S + s, lg - r * kWgs, s, S, length, in, out + (long)sig * length, tws,
+                                     lds);
+}
+
+// The inverse column pass alone, in the shape inv_passes picks for the batch.
+static int col_inv_pass(const float2* f, float2* work, const float2* twp, const float2* twh, const int* ovf,
+                        const float2* tws, int64_t batch, hipStream_t stream) {
+    if (batch <= kNarrowMaxBatch)
+        hipLaunchKernelGGL((k_col_inv<kInvColsNarrow, false>), dim3((unsigned)(batch * (256 / kInvColsNarrow))),
+                           dim3(8 * kInvColsNarrow), 0, stream, f, work, twp, twh, ovf, tws);
+    else if (batch <= kInvWriteThroughMaxBatch)
+        hipLaunchKernelGGL((k_col_inv<kInvColsWide, true>), dim3((unsigned)(batch * (256 / kInvColsWide))),
+                           dim3(8 * kInvColsWide), 0, stream, f, work, twp, twh, ovf, tws);
+    else
+        hipLaunchKernelGGL((k_col_inv<kInvColsWide, false>), dim3((unsigned)(batch * (256 / kInvColsWide))),
+                           dim3(8 * kInvColsWide), 0, stream, f, work, twp, twh, ovf, tws);
+    return launch_status();
+}
+
+// Both parities of the fused row pass: the even slices' launch, then the odd.
+template <int RPW, bool PAIR>
+static int row_inv_ola_passes(const float2* work, float* out, const float2* tws, int64_t nsig, int64_t S,
+                              int64_t length, hipStream_t stream) {
+    constexpr int kWgs = 128 / RPW;
+    const int64_t even = (S + 1) / 2, odd = S / 2;
+    hipLaunchKernelGGL((k_row_inv_ola<RPW, false, PAIR>), dim3((unsigned)(nsig * even * kWgs)), dim3(16 * RPW), 0,
+                       stream, work, out, tws, (int)S, (long)length, (int)even);
+    if (int e = launch_status()) return e;
+    if (odd == 0) return FCQT_OK;
+    hipLaunchKernelGGL((k_row_inv_ola<RPW, true, PAIR>), dim3((unsigned)(nsig * odd * kWgs)), dim3(16 * RPW), 0,
+                       stream, work, out, tws, (int)S, (long)length, (int)odd);
+    return launch_status();
+}
+
 }  // namespace fcqt
 
 using namespace fcqt;
+
+extern "C" int fcqt_sliced_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
+                                     const int32_t* ovf, const float* coef, float* f, float* work, float* out,
+                                     int64_t nsig, int64_t nslices, int64_t length, hipStream_t stream) {
+    if (!scat || !groups || !ovf || !coef || !f || !work || !out) return FCQT_EARG;
+    if (nsig < 1 || nslices < 1 || nsig > kMaxBatch || nslices > kMaxBatch || nsig * nslices > kMaxBatch)
+        return FCQT_EARG;
+    if (length < 1 || length > nslices * 2 * (int64_t)kQuarter) return FCQT_EARG;
+    const int64_t batch = nsig * nslices;
+    // every step's arguments before the first launch
+    if (int e = check_band_args(tab, scat, coef, coef, FCQT_INTERLEAVED, batch)) return e;
+    if (!tab->tw_pass || !tab->tw_half || !tab->tw_stage) return FCQT_EARG;
+    if (!aligned(f, 16) || !aligned(groups, 16) || !aligned(work, 8) || !aligned(ovf, 4) || !aligned(out, 4) ||
+        !aligned(tab->tw_pass, 8) || !aligned(tab->tw_half, 8) || !aligned(tab->tw_stage, 16))
+        return FCQT_EALIGN;
+    if (int e = fcqt_scatter_bands_sliced(tab, scat, groups, coef, f, nsig, nslices, 0, stream)) return e;
+    const auto* tws = reinterpret_cast<const float2*>(tab->tw_stage);
+    auto* w2 = reinterpret_cast<float2*>(work);
+    if (int e = col_inv_pass(reinterpret_cast<const float2*>(f), w2, reinterpret_cast<const float2*>(tab->tw_pass),
+                             reinterpret_cast<const float2*>(tab->tw_half), reinterpret_cast<const int*>(ovf), tws,
+                             batch, stream))
+        return e;
+    const bool pair = length % 2 == 0 && aligned(out, 8);
+    if (batch <= kNarrowMaxBatch)
+        return pair ? row_inv_ola_passes<kRowsNarrow, true>(w2, out, tws, nsig, nslices, length, stream)
+                    : row_inv_ola_passes<kRowsNarrow, false>(w2, out, tws, nsig, nslices, length, stream);
+    return pair ? row_inv_ola_passes<kRowsWide, true>(w2, out, tws, nsig, nslices, length, stream)
+                : row_inv_ola_passes<kRowsWide, false>(w2, out, tws, nsig, nslices, length, stream);
+}
 
 extern "C" int fcqt_packed_fft_fwd(const fcqt_tables* tab, const float* x, float* xs, float* work,
                                    int64_t batch, hipStream_t stream) {

@@ -12,7 +12,7 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 SYNC_PER_SLICE = 64       # FCQT_SYNC_PER_SLICE: uint32 per slice in a single-launch counter buffer
 PLANAR = 0
 INTERLEAVED = 1
@@ -24,7 +24,8 @@ EXPORTS = ("fcqt_abi_version", "fcqt_status_string", "fcqt_last_hip_error",
            "fcqt_slice_fft_fwd", "fcqt_route_bands_sliced", "fcqt_scatter_bands_sliced",
            "fcqt_overlap_add", "fcqt_stream_overlap", "fcqt_image_check", "fcqt_tables_upload",
            "fcqt_workspace_sizes", "fcqt_analysis_static", "fcqt_persist_analysis", "fcqt_persist_synthesis",
-           "fcqt_stream_analysis", "fcqt_stream_synthesis", "fcqt_sliced_analysis")
+           "fcqt_stream_analysis", "fcqt_stream_synthesis", "fcqt_sliced_analysis",
+           "fcqt_sliced_synthesis")
 
 
 class Tables(ctypes.Structure):
@@ -107,6 +108,7 @@ def _open(path):
         "fcqt_slice_fft_fwd": ([T, P, I64, P, I64, I64, I64, I64, P, P, S], ctypes.c_int),
         "fcqt_route_bands_sliced": ([T, P, P, P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_sliced_analysis": ([T, P, P, P, I64, P, I64, I64, P, P, P, S], ctypes.c_int),
+        "fcqt_sliced_synthesis": ([T, P, P, P, P, P, P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_scatter_bands_sliced": ([T, P, P, P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_overlap_add": ([P, P, I64, I64, I64, S], ctypes.c_int),
         "fcqt_stream_overlap": ([P, P, P, I64, I64, S], ctypes.c_int),

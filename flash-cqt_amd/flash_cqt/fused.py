@@ -308,6 +308,22 @@ class FusedOctCQT:
                                                     _native.ptr(xs), _native.ptr(work),
                                                     _native.stream_handle(self.dev.index)), "sliced_analysis")
 
+    def sliced_synthesis(self, coef, f, work, out, nsig, nslices, length, table="scat"):
+        """scatter_bands_sliced, the inverse passes and overlap_add of whole
+        signals in one call (fcqt_sliced_synthesis: the overlap-add happens
+        in the inverse row pass's store, same bits): out [nsig, length]."""
+        B = nsig * nslices
+        self._need(coef, B * self.ncoef * 8, "coef")
+        self._need(f, B * T.FROW * 8, "f")
+        self._need(work, B * L * 8, "work")
+        self._need(out, nsig * length * 4, "out")
+        _native.check(self.lib.fcqt_sliced_synthesis(self._ct, _native.ptr(self.tables[table]),
+                                                     _native.ptr(self.tables["slice_groups"]),
+                                                     _native.ptr(self.tables["ovf_" + table]), _native.ptr(coef),
+                                                     _native.ptr(f), _native.ptr(work), _native.ptr(out), nsig,
+                                                     nslices, length, _native.stream_handle(self.dev.index)),
+                      "sliced_synthesis")
+
     def scatter_bands_sliced(self, coef, f, nsig, nslices, table="scat", first=0):
         B = nsig * nslices
         self._need(coef, B * self.ncoef * 8, "coef")

@@ -16,10 +16,11 @@ pure-torch one. Assigning self.cqt swaps engines as in the reference.
 With the HIP engine and no gradient to record, fwd and bwd run the framing
 inside the engine's kernels (fcqt_sliced_analysis, which frames, transforms
 and routes, in chunks of about 128 slices from 256 slices on;
-fcqt_scatter_bands_sliced, fcqt_overlap_add): slices are read straight from
-the signal, coefficients are written and read in the block layout with the
-quarter roll applied, and the inverse slices are rolled and overlap-added
-in one pass. Blocks returned by that path are views of one buffer; passing
+fcqt_scatter_bands_sliced, the inverse passes and fcqt_overlap_add, or from
+256 slices on fcqt_sliced_synthesis, which overlap-adds in the inverse row
+pass's store): slices are read straight from the signal, coefficients are
+written and read in the block layout with the quarter roll applied, and the
+inverse slices are rolled and overlap-added in one pass. Blocks returned by that path are views of one buffer; passing
 them back to bwd reads that buffer without a copy. The bounded-state stream
 (stream_fwd / stream_bwd) runs each step as one C-ABI call per direction
 (fcqt_stream_analysis reads the carried half slice and the new chunk in place,
@@ -33,6 +34,17 @@ from . import _native
 
 from .ref_util import hann_fft_order
 from .oct_cqt import OctCQT
+
+
+# From this many slices on the whole-signal synthesis overlap-adds in the
+# inverse row pass (fcqt_sliced_synthesis); below, the slices go through a
+# slice buffer and one overlap-add kernel, which measured faster there
+# (SlicedCQT.bwd, fused against buffered): 53 against 49 us at 64 slices;
+# at configs[4]'s 120 slices the two row-pass launches took 8.4 + 12.7 us
+# against 11.3 + 8.2 us for the row pass and the overlap-add; 170 against
+# 179 us at 256 slices and 327-336 against 353-364 us at 512. Same bits
+# either way.
+FUSED_OLA_MIN_SLICES = 256
 
 
 def makewnd(sl_len, tr_area, device="cpu", dtype=torch.float32):
@@ -210,17 +222,20 @@ class SlicedCQT:
             self.__dict__.update(_cache_owner=f, _fused_ws={}, _stream_ptr_cache={})
         return self.__dict__["_fused_ws"], self.__dict__["_stream_ptr_cache"]
 
-    def _ws(self, f, nsig, S):
-        """Engine buffers for nsig * S slice rows. There is one buffer set per
-        engine, sized to the largest row count seen so far; a smaller call
-        uses its leading rows. Rows are independent, and F is only ever used
-        with the synthesis scatter table, so the slots that table never
-        writes stay zero in every row (F is zeroed when allocated). Memory is
-        therefore bounded by the largest call, whatever the signal lengths.
+    def _ws(self, f, nsig, S, y=False):
+        """Engine buffers for nsig * S slice rows: X, W, F, and with y=True
+        (the streamed synthesis) a slice buffer Y; the whole-signal
+        synthesis overlap-adds inside its row pass and needs none. There is
+        one buffer set per engine, sized to the largest row count seen so
+        far (Y to the largest streamed row count); a smaller call uses its
+        leading rows. Rows are independent, and F is only ever used with the
+        synthesis scatter table, so the slots that table never writes stay
+        zero in every row (F is zeroed when allocated). Memory is therefore
+        bounded by the largest call, whatever the signal lengths.
 
-        A set that served a call under stream capture (hipGraph) stays
-        allocated after a larger set replaces it: the recorded launches hold
-        its addresses and write into it on every replay."""
+        A set (or a Y) that served a call under stream capture (hipGraph)
+        stays allocated after a larger one replaces it: the recorded launches
+        hold its addresses and write into it on every replay."""
         cache, ptrs = self._caches(f)
         B = nsig * S
         full = cache.get("rows")
@@ -233,11 +248,15 @@ class SlicedCQT:
             ptrs.clear()                 # cached raw pointers refer to the old buffers
             cache["rows"] = full = dict(B=B, captured=False, X=torch.empty(B, T.XSTRIDE, 2, device=dev),
                                         W=torch.empty(B, T.L, 2, device=dev),
-                                        F=slot_buffer(B, dev),
-                                        Y=torch.empty(B, self.sl_len, device=dev))
+                                        F=slot_buffer(B, dev))
+        if y and ("Y" not in full or full["Y"].shape[0] < B):
+            if "Y" in full and full["captured"]:
+                cache.setdefault("recorded", []).append({"Y": full["Y"]})
+            ptrs.clear()
+            full["Y"] = torch.empty(B, self.sl_len, device=f.dev)
         if torch.cuda.is_current_stream_capturing():
             full["captured"] = True
-        return {k: full[k][:B] for k in ("X", "W", "F", "Y")}
+        return {k: full[k][:B] for k in (("X", "W", "F", "Y") if y else ("X", "W", "F"))}
 
     def _tw32(self):
         tw = self.__dict__.get("_tw32_cache")
@@ -285,12 +304,18 @@ class SlicedCQT:
         S = blocks[0].shape[-1] // self.size_per_oct[0]
         nsig = B * C
         coef = self._block_buffer(f, blocks, side, nsig, S)
-        ws = self._ws(f, nsig, S)
-        f.scatter_bands_sliced(coef, ws["F"], nsig, S)
-        f.packed_ifft(ws["F"], ws["Y"], ws["W"])
         n = S * 2 * self.H if length is None else min(int(length), S * 2 * self.H)
         out = torch.empty(B, C, n, dtype=torch.float32, device=f.dev)
-        f.overlap_add(ws["Y"], out, nsig, S, n)
+        if nsig * S >= FUSED_OLA_MIN_SLICES:
+            # scatter, inverse passes and the overlap-add (in the row pass's
+            # store) in one call; no slice buffer
+            ws = self._ws(f, nsig, S)
+            f.sliced_synthesis(coef, ws["F"], ws["W"], out, nsig, S, n)
+        else:
+            ws = self._ws(f, nsig, S, y=True)
+            f.scatter_bands_sliced(coef, ws["F"], nsig, S)
+            f.packed_ifft(ws["F"], ws["Y"], ws["W"])
+            f.overlap_add(ws["Y"], out, nsig, S, n)
         return out
 
     # --------------------------------------------------- whole buffer api
@@ -345,7 +370,7 @@ class SlicedCQT:
         bufs, cache = self._caches(f)
         st = cache.get(nsig)
         if st is None:
-            st = {k: v.data_ptr() for k, v in self._ws(f, nsig, 1).items()}
+            st = {k: v.data_ptr() for k, v in self._ws(f, nsig, 1, y=True).items()}
             st["tw"] = self._tw32().data_ptr()
             cache[nsig] = st
         elif torch.cuda.is_current_stream_capturing():

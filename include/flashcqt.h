@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 11
+#define FCQT_ABI_VERSION 12
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -337,6 +337,21 @@ int fcqt_sliced_analysis(const fcqt_tables* tab, const int32_t* route, const int
 int fcqt_scatter_bands_sliced(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
                               const float* coef, float* f, int64_t nsig, int64_t nslices, int64_t first,
                               hipStream_t stream);
+
+/* The whole-signal sliced synthesis in one call, with the overlap-add in the
+ * inverse row pass: fcqt_scatter_bands_sliced (first = 0), the inverse column
+ * pass, then the inverse row pass twice, over the even slices (storing into
+ * out) and over the odd ones (adding to it), so no [nslices][65536] slice
+ * buffer is written or read back. The same output bits as
+ * fcqt_scatter_bands_sliced + fcqt_packed_fft_inv + fcqt_overlap_add.
+ *   coef   nsig * nslices * ncoef complex, the block layout
+ *   f      [nsig * nslices][FCQT_FROW] complex (F rules as fcqt_scatter_bands)
+ *   work   [nsig * nslices][32768] complex scratch
+ *   out    [nsig][length] fp32, length <= nslices * 32768
+ * Replaces SlicedCQT.bwd (sliced.py:148-167) for whole signals. */
+int fcqt_sliced_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* groups,
+                          const int32_t* ovf, const float* coef, float* f, float* work, float* out,
+                          int64_t nsig, int64_t nslices, int64_t length, hipStream_t stream);
 
 /* Overlap-add of the inverse slices (y [nsig * nslices][65536], the output of
  * fcqt_packed_fft_inv): out[sig][p], p < length <= nslices * 2H, sums the

@@ -592,6 +592,46 @@ def overlap_add(y, nsig, S, length, vec4=False):
     return out
 
 
+def row_inv_ola(y, nsig, S, length):
+    """The inverse row pass with the overlap-add fused into its store
+    (k_row_inv_ola): a launch over the even slices, then one over the odd
+    slices. Slice s's sample jj goes to p = 2H (s - 1) + j, j = (jj + H) mod N
+    (even s) or (jj - H) mod N (odd s), if 0 <= p < length. Even slices store
+    0 + v; odd slices add to what the even launch stored, except in their
+    second half when no slice s + 1 exists, where they store 0 + v. Asserts
+    every output sample is stored exactly once before it is added to, and at
+    most once added to, in launch order."""
+    H = N // 4
+    hop = 2 * H
+    out = np.full((nsig, length), np.nan, np.float32)
+    stored = np.zeros((nsig, length), np.int64)
+    added = np.zeros((nsig, length), np.int64)
+    jj = np.arange(N)
+    for odd in (0, 1):
+        for sig in range(nsig):
+            for s in range(odd, S, 2):
+                j = (jj + (N - H if odd else H)) & (N - 1)
+                p = hop * (s - 1) + j
+                ok = (p >= 0) & (p < length)
+                v = y[sig * S + s][ok].astype(np.float32)
+                pp = p[ok]
+                if odd:
+                    add = (j[ok] < hop) | (s + 1 < S)
+                    assert (stored[sig, pp[add]] == 1).all() and (added[sig, pp[add]] == 0).all()
+                    out[sig, pp[add]] = out[sig, pp[add]] + v[add]
+                    added[sig, pp[add]] += 1
+                    st = ~add
+                    assert (stored[sig, pp[st]] == 0).all()
+                    out[sig, pp[st]] = np.float32(0) + v[st]
+                    stored[sig, pp[st]] += 1
+                else:
+                    assert (stored[sig, pp] == 0).all()
+                    out[sig, pp] = np.float32(0) + v
+                    stored[sig, pp] += 1
+    assert (stored == 1).all()
+    return out
+
+
 def stream_overlap(y, tail, k):
     """k_stream_overlap: y [nsig, N] one inverse slice k per signal; returns
     (out or None, new tail)."""

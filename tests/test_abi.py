@@ -46,7 +46,7 @@ def test_variant_library_exports_the_same_abi():
 
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 11
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 12
 
 
 def test_header_constants_match_tables_and_kernels():
@@ -131,6 +131,13 @@ def test_argument_errors_detected_before_any_launch(lib):
     assert lib.fcqt_sliced_analysis(T, p, p, p, 100, p, 1 << 12, 1 << 12, p, p, p, s) == EARG  # too many rows
     assert lib.fcqt_sliced_analysis(T, p, p, p, 100, p, 1, 1, p, p, null, s) == EARG           # no work buffer
     assert lib.fcqt_sliced_analysis(T, p, ctypes.c_void_p(4104), p, 100, p, 1, 1, p, p, p, s) == EALIGN
+    # whole-signal sliced synthesis: (tab, scat, groups, ovf, coef, f, work, out, nsig, nslices, length, stream)
+    assert lib.fcqt_sliced_synthesis(T, p, p, p, p, p, p, null, 1, 1, 100, s) == EARG          # no output
+    assert lib.fcqt_sliced_synthesis(T, p, p, p, p, p, p, p, 1, 1, 32769, s) == EARG           # longer than 2H
+    assert lib.fcqt_sliced_synthesis(T, p, p, p, p, p, p, p, 1, 1, 0, s) == EARG               # empty output
+    assert lib.fcqt_sliced_synthesis(T, p, p, p, p, p, p, p, 0, 1, 100, s) == EARG             # no signals
+    assert lib.fcqt_sliced_synthesis(T, p, p, p, p, odd, p, p, 1, 1, 100, s) == EALIGN         # F alignment
+    assert lib.fcqt_sliced_synthesis(T, p, p, p, p, p, p, ctypes.c_void_p(4098), 1, 1, 100, s) == EALIGN
     assert lib.fcqt_overlap_add(p, p, 1, 1, 2 * 32768 + 1, s) == EARG      # longer than nslices * 2H
     assert lib.fcqt_overlap_add(p, null, 1, 1, 10, s) == EARG
     assert lib.fcqt_fill_zero(p, 0, s) == 0  # nothing to do, no launch
@@ -154,6 +161,7 @@ def test_coefficient_span_beyond_ncoef_is_refused(lib):
         assert lib.fcqt_analysis(tab, p, p, p, p, 0, p, p, 1, s) == 1
         assert lib.fcqt_synthesis(tab, p, p, p, p, 0, p, p, p, 1, s) == 1
         assert lib.fcqt_sliced_analysis(tab, p, p, p, 100, p, 1, 1, p, p, p, s) == 1
+        assert lib.fcqt_sliced_synthesis(tab, p, p, p, p, p, p, p, 1, 1, 100, s) == 1
 
 
 def test_static_analysis_argument_errors_before_any_launch(lib):

@@ -734,6 +734,59 @@ def test_sliced_chunked_analysis_same_bits(fused, nsig, S):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("nsig,S,length", [(1, 1, 1000), (3, 5, 7), (2, 20, 17 * 32768 + 3), (2, 4, 2 * 32768),
+                                           (8, 15, 441000), (1, 2, 32769), (4, 40, 39 * 32768 + 100)])
+def test_sliced_synthesis_fused_overlap_add_same_bits(fused, nsig, S, length):
+    """fcqt_sliced_synthesis (even slices stored, odd slices added, in the
+    inverse row pass's store) gives the bits of scatter + inverse passes +
+    k_overlap_add, signed zeros included: one slice, slices past the end of
+    a short output, odd lengths (4-byte stores) and even ones (8-byte)."""
+    rs = np.random.RandomState(19)
+    B = nsig * S
+    coef = torch.from_numpy((rs.standard_normal((B * fused.ncoef,)) + 1j * rs.standard_normal((B * fused.ncoef,)))
+                            .astype(np.complex64)).to(_dev())
+    from flash_cqt import tables as T
+    from flash_cqt.fused import slot_buffer
+    f1, f2 = slot_buffer(B, _dev()), slot_buffer(B, _dev())
+    work = torch.empty(B, 32768, 2, device=_dev())
+    y = torch.empty(B, N, device=_dev())
+    ref = torch.full((nsig, length), float("nan"), device=_dev())
+    fused.scatter_bands_sliced(coef, f1, nsig, S)
+    fused.packed_ifft(f1, y, work)
+    fused.overlap_add(y, ref, nsig, S, length)
+    got = torch.full((nsig, length), float("nan"), device=_dev())
+    fused.sliced_synthesis(coef, f2, work, got, nsig, S, length)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), ref.view(torch.int32))
+
+
+def test_sliced_long_signals_round_trip():
+    """SlicedCQT on 2 x 160 slices (the chunked analysis and, from 256
+    slices on, the overlap-add in the row pass): round trip >= 125 dB, and
+    the inverse equal to the slice-buffer path's (scatter, inverse passes,
+    overlap-add kernel) bit for bit."""
+    from flash_cqt import SlicedCQT
+    from flash_cqt import sliced as sl
+    s = SlicedCQT(device=_dev())
+    hop = N // 2
+    length = 158 * hop + 999
+    assert s._num_slices(length) == 160
+    x = torch.randn(1, 2, length, generator=torch.Generator().manual_seed(23)).to(_dev())
+    with torch.no_grad():
+        bl, sd = s.fwd(x)
+        y = s.bwd(bl, sd, length=length).clone()
+        assert 2 * 160 >= sl.FUSED_OLA_MIN_SLICES
+        keep = sl.FUSED_OLA_MIN_SLICES
+        try:
+            sl.FUSED_OLA_MIN_SLICES = 1 << 30              # force the slice-buffer path
+            y2 = s.bwd(bl, sd, length=length)
+        finally:
+            sl.FUSED_OLA_MIN_SLICES = keep
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    assert snr_db(x.double().cpu().numpy(), y.double().cpu().numpy()) >= 125
+
+
 @pytest.mark.parametrize("length", [1, 1000, 16384, 32768, 32769, 65536, 131071, 262144])
 def test_sliced_fused_ragged_lengths(length):
     """Short, hop-aligned and ragged signal lengths, two channels: the fused

@@ -239,6 +239,27 @@ def test_overlap_add_index_math_cpu():
             assert np.array_equal(ks.overlap_add(y, 2, S, length, vec4=True), ref)
 
 
+def test_fused_row_overlap_add_index_math_cpu():
+    """The inverse row pass with the overlap-add in its store (even slices,
+    then odd ones) writes every output sample once before adding to it, and
+    gives k_overlap_add's bits, signed zeros included, for ragged lengths,
+    one slice, and slices past the end of the signal."""
+    N, H = ks.N, ks.N // 4
+    rs = np.random.RandomState(6)
+    cases = [(8, None), (1000, None), (3 * 2 * H + 12, None), (5 * 2 * H, None), (2 * H - 2, None),
+             (1000, 1), (2 * H, 1), (2 * H + 1, 2), (7, 5)]
+    for length, S in cases:
+        if S is None:
+            quarters = -(-length // H)
+            S = (quarters + 1) // 2 + 1
+        y = rs.standard_normal((2 * S, N)).astype(np.float32)
+        y[:, ::97] = np.float32(-0.0)                 # exact zeros of both signs
+        y[:, 1::89] = np.float32(0.0)
+        ref = ks.overlap_add(y, 2, S, length)
+        got = ks.row_inv_ola(y, 2, S, length)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (length, S)
+
+
 def test_stream_overlap_index_math_cpu():
     """The streamed overlap-add kernel's indexing equals the reference's roll
     by +H (even slices) / -H (odd) and half-slice overlap-add."""
@@ -302,7 +323,14 @@ def test_sliced_buffer_sets_kept_for_recorded_graphs_cpu(monkeypatch):
     capturing[0] = False
     third_call = s._ws(f, 2, 2)                          # grows again
     assert s._fused_ws["recorded"] == [second] and s._fused_ws["rows"]["B"] == 4
-    assert third_call["Y"].shape == (4, T.N)
+    assert "Y" not in third_call and "Y" not in s._fused_ws["rows"]   # the whole-signal path needs no Y
+    assert s._ws(f, 3, 1, y=True)["Y"].shape == (3, T.N)           # the streamed synthesis gets one
+    y3 = s._fused_ws["rows"]["Y"]
+    capturing[0] = True
+    s._ws(f, 3, 1, y=True)
+    capturing[0] = False
+    s._ws(f, 4, 1, y=True)                               # a larger Y: the recorded one is kept
+    assert s._fused_ws["recorded"][-1]["Y"] is y3 and s._fused_ws["rows"]["Y"].shape == (4, T.N)
     # the streamed path marks the set it hands out cached pointers for
     s._stream_ptrs = SlicedCQT._stream_ptrs.__get__(s)
     s._tw32 = lambda: torch.zeros(1)
