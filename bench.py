@@ -15,7 +15,8 @@ configs[2]); batch 1 (configs[1], sinusoids + noise) and batch 16 are in
     hipFFT/rocFFT) on the GPU, graph-captured, same inputs;
   - the host-core baseline: the oracle's torch port of the reference
     OctCQT on the box's CPU cores, a bounded sample (cpu_baseline);
-  - the SlicedCQT streaming workload (configs[4]) in "sliced";
+  - the SlicedCQT streaming workload in "sliced", with a long
+    signal (512 slices) in "sliced.long_signal";
   - the TrainableCQT differentiable step in "training_step".
 Per-kernel launch durations are timed with hipEvents on the launch stream
 around back-to-back stream launches (graphs of the same launches beside
@@ -239,6 +240,47 @@ def sliced_workload(dev):
     log(f"sliced: {ms:.4f} ms  {res['msamples_per_s']:.0f} Msamples/s  rt {res['roundtrip_snr_db']:.1f} dB"
         f"  (host framing {msc:.4f} ms); streamed: {mss:.3f} ms  (host framing {mss_host:.3f} ms)"
         f"  rt {res['stream_roundtrip_snr_db']:.1f} dB")
+    return res
+
+
+def sliced_long(dev):
+    """A long signal: SlicedCQT on one signal of 512 slices (16.8 M samples,
+    6.3 min at 44.1 kHz), fwd and bwd each timed as the product runs them
+    (framing + route in chunks of about 128 slices; overlap-add in the
+    inverse row pass) and, in the same run, in their one-call forms (framing
+    pass + route over all slices; slice buffer + overlap-add kernel)."""
+    from flash_cqt import SlicedCQT
+    from flash_cqt import sliced as sl
+    s = SlicedCQT(fs=FS, device=dev)
+    S = 512
+    L = (S - 2) * s.hop + 1000
+    assert s._num_slices(L) == S
+    x = torch.randn(1, 1, L, generator=torch.Generator().manual_seed(3)).to(dev)
+    f = s.cqt.f
+    with torch.no_grad():
+        bl, sd = s.fwd(x)
+        y = s.bwd(bl, sd, length=L)
+        res = {"workload": "SlicedCQT, one signal of 512 slices (16.8 M samples)", "slices": S,
+               "roundtrip_snr_db": snr_db(x, y)}
+        res["fwd_ms"] = per_step_ms(lambda: s.fwd(x), steps=10, warm=2)
+        res["bwd_ms"] = per_step_ms(lambda: s.bwd(bl, sd, length=L), steps=10, warm=2)
+        ws = s._ws(f, 1, S)
+        coef = torch.empty(S * f.ncoef, dtype=torch.complex64, device=dev)
+        sig = x.reshape(1, L)
+
+        def fwd_one_call():
+            f.slice_fft(sig, s._tw32(), S, ws["X"], ws["W"])
+            f.route_bands_sliced(ws["X"], coef, 1, S)
+        res["fwd_one_call_ms"] = per_step_ms(fwd_one_call, steps=10, warm=2)
+        keep = sl.FUSED_OLA_MIN_SLICES
+        sl.FUSED_OLA_MIN_SLICES = 1 << 30          # the slice-buffer synthesis
+        try:
+            res["bwd_slice_buffer_ms"] = per_step_ms(lambda: s.bwd(bl, sd, length=L), steps=10, warm=2)
+        finally:
+            sl.FUSED_OLA_MIN_SLICES = keep
+    log(f"sliced long signal ({S} slices): fwd {res['fwd_ms']:.3f} ms (one call {res['fwd_one_call_ms']:.3f}),"
+        f" bwd {res['bwd_ms']:.3f} ms (slice buffer {res['bwd_slice_buffer_ms']:.3f}),"
+        f" rt {res['roundtrip_snr_db']:.1f} dB")
     return res
 
 
@@ -785,6 +827,7 @@ def main():
                "traffic_source": "sum over the six kernels in profiles/hbm_traffic_b64.txt" if rt_traffic else None}
 
     sliced = sliced_workload(dev)
+    sliced["long_signal"] = sliced_long(dev)
     exchange = band_exchange(f)
     train = training_step(dev, cqt_gpu)
     mem = peak_memory(cqt_gpu, dev)
