@@ -785,6 +785,17 @@ def test_sliced_long_signals_round_trip():
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
     assert snr_db(x.double().cpu().numpy(), y.double().cpu().numpy()) >= 125
+    # both long-signal forms (chunked analysis, overlap-add in the row pass)
+    # replay in a graph to the eager result, with eager work in between
+    from flash_cqt import Graphed
+    with torch.no_grad():
+        g = Graphed(lambda a: s.bwd(*s.fwd(a), length=length), x)
+        for _ in range(3):
+            yg = g(x)
+            torch.cuda.synchronize()
+            assert torch.equal(yg.view(torch.int32), y.view(torch.int32))
+            s.fwd(x[..., :5 * hop])
+            torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("length", [1, 1000, 16384, 32768, 32769, 65536, 131071, 262144])
