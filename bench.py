@@ -26,7 +26,8 @@ over its duration against 8 TB/s.
 Extra modes (for rocprofv3 counter runs): --kernels-only runs a few
 launches of every kernel plus a plain copy of known size (the calibration
 kernel for FETCH_SIZE / WRITE_SIZE) and prints nothing else; --sliced-only
-runs the SlicedCQT workload alone and prints its JSON object.
+runs the SlicedCQT workload alone and prints its JSON object;
+--sliced-long-only does the same for the long-signal measurement.
 """
 import argparse
 import json
@@ -695,6 +696,7 @@ def main():
     ap.add_argument("--no-lib-baseline", action="store_true")
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--sliced-only", action="store_true")
+    ap.add_argument("--sliced-long-only", action="store_true")
     ap.add_argument("--no-single-launch", action="store_true",
                     help="skip the single-launch (cooperative) directions")
     ap.add_argument("--single-launch-only", action="store_true",
@@ -722,6 +724,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.sliced_only:
         print(json.dumps(json_safe(sliced_workload(dev))), flush=True)
+        return
+    if args.sliced_long_only:
+        print(json.dumps(json_safe(sliced_long(dev))), flush=True)
         return
     cqt_gpu = OctCQT([3, 4, 2], [8, 16, 32], fs=FS, audio_len=N, device=dev)
     f = FusedOctCQT(cqt_gpu, dev)
