@@ -1,16 +1,19 @@
 """Flexible octave filterbank of the octave-mode CQT: centre frequencies,
 window lengths, per-octave block lengths, analysis and dual windows.
 
-Follows filterbank.py:84-177 of the reference so that every table is
-bit-identical (pinned by tests against golden vectors recorded from the
-reference). Two details of that recipe are reproduced on purpose:
+Follows FlexOctBank, filterbank.py:26-122 of the reference, so that every
+table is bit-identical (pinned by tests against golden vectors recorded from
+the reference). Two details of that recipe are reproduced on purpose:
   * the per-octave power-of-two block length is also written into the
     mirrored half of the length vector one position too low
-    (filterbank.py:165), so the Nyquist side band gets the top octave's
-    block length (2048 for [3,4,2]/[8,16,32]) and the frame diagonal is
-    weighted with that shifted vector;
+    (filterbank.py:110), so the Nyquist side band gets the top octave's
+    block length (2048 for [3,4,2]/[8,16,32], read at filterbank.py:122) and
+    the frame diagonal is weighted with that shifted vector;
   * windows are built from the un-rounded lengths, only the block lengths
-    are rounded to powers of two.
+    are rounded to powers of two (roundings at filterbank.py:74-76, 85-94).
+The windows and the frame diagonal are built in the bank's dtype, as the
+reference's hannwin(...).to(dtype) and nsdual(dtype=...) do
+(filterbank.py:114-117): float32 by default, float64 for a float64 bank.
 """
 import math
 
@@ -111,10 +114,15 @@ class FlexOctBank:
 
         self.np_M = M.astype(np.int64)
         self.np_M_raw = M_raw
-        self.np_g = [hann_fft_order(int(m)).astype(np.float32) for m in M_raw]
+        # window values in the bank's dtype: float64 stays as built, every
+        # other dtype is built from float32 windows (the reference's
+        # .to(dtype) of the float64 window), then cast on the device
+        self.np_dtype = np.float64 if dtype == torch.float64 else np.float32
+        self.np_g = [hann_fft_order(int(m)).astype(self.np_dtype) for m in M_raw]
         self.np_wins, self.nn = window_ranges([len(g) for g in self.np_g], rpos, audio_len)
         assert self.nn == audio_len
-        self.np_gd, self.np_diag = painless_dual(self.np_g, self.np_wins, self.nn, self.np_M)
+        self.np_gd, self.np_diag = painless_dual(self.np_g, self.np_wins, self.nn, self.np_M,
+                                                 dtype=self.np_dtype)
 
         dev = self.device
         self.M = torch.as_tensor(self.np_M, dtype=torch.int64, device=dev)

@@ -393,7 +393,7 @@ class FusedOctCQT:
 
     def persist_fwd(self, x):
         """The reference's single-launch forward (fused.py:748-762,
-        persist2.cu:140-175): the whole analysis as one launch
+        persist2.cu:140-161): the whole analysis as one launch
         (fcqt_persist_analysis: column tiles, row tiles and band tasks of a
         slice on one XCD, each stage waiting for the slice's previous one).
         Same outputs as fwd, bit for bit (workspace views)."""
@@ -409,7 +409,7 @@ class FusedOctCQT:
 
     def persist_inv(self, KR, KI):
         """The reference's single-launch inverse (fused.py:764-778,
-        persist2.cu:177-222): the whole synthesis as one launch
+        persist2.cu:163-222): the whole synthesis as one launch
         (fcqt_persist_synthesis: band scatter, inverse column tiles and
         inverse row tiles of a slice on one XCD, each stage waiting for the
         slice's previous one). Same output as bwd, bit for bit (a workspace

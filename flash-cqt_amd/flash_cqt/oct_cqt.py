@@ -22,16 +22,19 @@ from .filterbank import FlexOctBank
 
 def _group_tables(bank, band_ids, Lo, nn):
     """Gather index, window, scatter position, dual window and conj mask of a
-    group of bands sharing block length Lo (numpy, float32 values).
+    group of bands sharing block length Lo (numpy; values in the bank's
+    dtype, float32 or float64, as the reference's enc_dec_group builds them
+    in self.dtype, oct_cqt.py:36-67).
 
     A window of length Lg centred on bin c is laid out in fft order inside
     the block: taps 0..r-1 hold bins c..c+r-1, taps Lo-l..Lo-1 hold bins
     c-l..c-1 (r = ceil(Lg/2), l = floor(Lg/2)); the rest stay zero.
     """
     nb = len(band_ids)
+    vt = bank.np_dtype
     idx = np.zeros((nb, Lo), dtype=np.int64)
-    gv = np.zeros((nb, Lo), dtype=np.float32)
-    gdv = np.zeros((nb, Lo), dtype=np.float32)
+    gv = np.zeros((nb, Lo), dtype=vt)
+    gdv = np.zeros((nb, Lo), dtype=vt)
     for k, bi in enumerate(band_ids):
         rng = bank.np_wins[bi]
         Lg = rng.shape[0]
@@ -39,14 +42,14 @@ def _group_tables(bank, band_ids, Lo, nn):
         centred = np.fft.fftshift(bank.np_g[bi])
         idx[k, :r], idx[k, Lo - l:] = rng[l:], rng[:l]
         gv[k, :r], gv[k, Lo - l:] = centred[l:], centred[:l]
-        dual = bank.np_gd[bi] * np.float32(Lo)
+        dual = bank.np_gd[bi] * vt(Lo)
         gdv[k, :r], gdv[k, Lo - l:] = dual[:r], dual[r:]
     half = nn // 2
     pos = idx.copy()
     conj = idx > half
     idx = np.where(conj, nn - idx, idx)
     live = pos <= half
-    gdv = (gdv * live).astype(np.float32)
+    gdv = (gdv * live).astype(vt)
     pos = np.where(live, pos, 0)
     return idx, gv, pos, gdv, conj
 

@@ -1,11 +1,13 @@
 """Window helpers of the nonstationary Gabor bank: Hann window, window index
 ranges and the painless dual frame.
 
-The numbers must be bit-identical to the reference bank (ref_util.py:19-55),
+The numbers must be bit-identical to the reference bank (ref_util.py:16-52),
 because the windows are the transform's definition: same float64 Hann
-recipe (scale, cos, +1, *0.5), same float32 frame diagonal accumulated band
-by band in band order. Everything is computed with numpy on the host and
-returned as numpy arrays; callers move the results to their device.
+recipe (scale, cos, +1, *0.5, ref_util.py:16-22), same frame diagonal
+accumulated band by band in band order, in the bank's dtype (float32 for a
+float32 bank, float64 for a float64 one, ref_util.py:43-52). Everything is
+computed with numpy on the host and returned as numpy arrays; callers move
+the results to their device.
 """
 import numpy as np
 
@@ -26,7 +28,7 @@ def window_ranges(lengths, centre_bins, total):
     Window i of length Lg is centred on its centre position and covers
     [centre - Lg//2, centre + Lg - Lg//2). The centre positions are the
     cumulative sum of the rounded centre-frequency increments, started at
-    the wrap-around increment of the last centre (ref_util.py:28-43).
+    the wrap-around increment of the last centre (ref_util.py:25-40).
     """
     inc = np.concatenate(((np.mod(-centre_bins[-1], total),), np.diff(centre_bins)))
     centres = np.cumsum(inc)
@@ -40,12 +42,12 @@ def window_ranges(lengths, centre_bins, total):
 
 
 def painless_dual(windows, ranges, nn, block_lengths, dtype=np.float32):
-    """Canonical dual windows of a painless frame (diagonal in `dtype`,
-    float32 as the reference bank uses).
+    """Canonical dual windows of a painless frame, computed in `dtype`
+    (the bank's dtype: float32 by default, float64 for a float64 bank).
 
     The frame operator is diagonal: d[k] = sum_i M_i |g_i(k)|^2 over the
     windows covering bin k (g in natural order), and the dual of window i is
-    g_i / d over its own support, back in fft order (ref_util.py:46-55).
+    g_i / d over its own support, back in fft order (ref_util.py:43-52).
     Returns (duals, diagonal).
     """
     d = np.zeros(nn, dtype=dtype)
@@ -57,14 +59,14 @@ def painless_dual(windows, ranges, nn, block_lengths, dtype=np.float32):
 
 # names the reference exports
 def hannwin(l, device="cpu"):
-    """Reference-compatible alias: float64 torch Hann window (ref_util.py:19)."""
+    """Reference-compatible alias: float64 torch Hann window (ref_util.py:16-22)."""
     import torch
     return torch.as_tensor(hann_fft_order(l), device=torch.device(device))
 
 
 def calcwinrange(g, rfbas, Ls, device="cpu"):
     """Reference-compatible: (index ranges as int64 tensors, nn) of windows g
-    centred at the bins rfbas (ref_util.py:28-43); window_ranges does the work."""
+    centred at the bins rfbas (ref_util.py:25-40); window_ranges does the work."""
     import torch
     ranges, nn = window_ranges([len(gi) for gi in g], np.asarray(rfbas), Ls)
     return [torch.as_tensor(r, device=torch.device(device)) for r in ranges], nn
@@ -72,7 +74,7 @@ def calcwinrange(g, rfbas, Ls, device="cpu"):
 
 def nsdual(g, wins, nn, M=None, dtype=None, device="cpu"):
     """Reference-compatible: dual windows (torch tensors) of windows g over
-    ranges wins with block lengths M (ref_util.py:46-55); the frame diagonal
+    ranges wins with block lengths M (ref_util.py:43-52); the frame diagonal
     accumulates in `dtype` (float32 by default, as the reference's)."""
     import torch
     if M is None:

@@ -5,7 +5,10 @@ cpu_baseline leg may use this module, and only as the checker.
 
 Tables (windows, dual windows, gather/scatter indices) are built in float32
 with the same operation order as the reference, so they are bit-identical to
-the reference's tables (pinned by tests/golden fixtures). The transforms
+the reference's tables (pinned by tests/golden fixtures); a float64 bank
+(dtype=np.float64, the reference's OctCQT(dtype=torch.float64)) is built the
+same way in float64 and pinned by the painless-frame identity and the
+round trip it then reconstructs to near machine precision. The transforms
 themselves are evaluated in float64 (numpy pocketfft), which makes this
 oracle more accurate than the reference's own float32 torch path: any
 implementation of the same algorithm in fp32 lands ~130-145 dB from it.
@@ -31,7 +34,8 @@ def snr_db(ref, test):
 def hannwin(l):
     """Hann window with its peak at index 0, float64.
 
-    Follows ref_util.py:19-25 (same operation order: scale, cos, +1, *0.5).
+    Follows hannwin, ref_util.py:16-22 (same operation order: scale, cos,
+    +1, *0.5).
     """
     r = np.arange(l, dtype=np.float64)
     r *= np.pi * 2. / l
@@ -44,7 +48,7 @@ def hannwin(l):
 def calcwinrange(lengths, rfbas, Ls):
     """Window index ranges (mod nn) and the total length nn.
 
-    Follows ref_util.py:28-43.
+    Follows calcwinrange, ref_util.py:25-40.
     """
     shift = np.concatenate(((np.mod(-rfbas[-1], Ls),), rfbas[1:] - rfbas[:-1]))
     timepos = np.cumsum(shift)
@@ -57,17 +61,18 @@ def calcwinrange(lengths, rfbas, Ls):
     return wins, int(nn)
 
 
-def nsdual(g, wins, nn, M):
-    """Painless dual windows in float32, frame operator diagonal weighted by M.
+def nsdual(g, wins, nn, M, dtype=np.float32):
+    """Painless dual windows in `dtype`, frame operator diagonal weighted by M.
 
-    Follows ref_util.py:46-55: the diagonal is accumulated band by band in
-    float32 in band order, then each window is divided by the ifftshifted
+    Follows nsdual, ref_util.py:43-52: the diagonal is accumulated band by
+    band in `dtype` (float32 for the default bank, float64 for a float64
+    one) in band order, then each window is divided by the ifftshifted
     diagonal over its own support.
     """
-    x = np.zeros(nn, dtype=np.float32)
+    x = np.zeros(nn, dtype=dtype)
     for gi, mii, sl in zip(g, M, wins):
         xa = np.square(np.fft.fftshift(gi))
-        xa = xa * np.float32(mii)
+        xa = xa * dtype(mii)
         x[sl] = x[sl] + xa
     gd = [gi / np.fft.ifftshift(x[wi]) for gi, wi in zip(g, wins)]
     return gd, x
@@ -82,13 +87,16 @@ def next_power_of_2(x):
 class FlexOctBank:
     """Analysis windows, dual windows and octave layout for one audio_len.
 
-    Follows filterbank.py:84-177, including the mirrored block-size write one
-    position too low (filterbank.py:165), which makes Mnyq the top octave's
-    block length (2048 for the [3,4,2]/[8,16,32] layout) and weights the
-    frame-operator diagonal with the shifted M vector.
+    Follows FlexOctBank, filterbank.py:26-122, including the mirrored
+    block-size write one position too low (filterbank.py:110), which makes
+    Mnyq (filterbank.py:122) the top octave's block length (2048 for the
+    [3,4,2]/[8,16,32] layout) and weights the frame-operator diagonal with
+    the shifted M vector. Windows and the diagonal are built in `dtype`
+    (filterbank.py:114-117: hannwin(...).to(dtype), nsdual(dtype=...)):
+    float32 by default, float64 for a float64 bank.
     """
 
-    def __init__(self, num_octs, bins_per_oct, fs, audio_len, min_win=4):
+    def __init__(self, num_octs, bins_per_oct, fs, audio_len, min_win=4, dtype=np.float32):
         if isinstance(num_octs, int):
             num_octs = [num_octs]
         if isinstance(bins_per_oct, int):
@@ -159,10 +167,11 @@ class FlexOctBank:
         self.M_raw = M_raw
         self.M = M.astype(np.int64)
         self.rfbas = rfbas
-        self.g = [hannwin(int(m)).astype(np.float32) for m in M_raw]
+        self.dtype = dtype
+        self.g = [hannwin(int(m)).astype(dtype) for m in M_raw]
         self.wins, self.nn = calcwinrange([len(gi) for gi in self.g], rfbas, audio_len)
         assert self.nn == audio_len
-        self.gd, self.diag = nsdual(self.g, self.wins, self.nn, self.M)
+        self.gd, self.diag = nsdual(self.g, self.wins, self.nn, self.M, dtype=dtype)
         self.fbins = lbas
         self.frqs_hz = frq / scale
         self.M0 = int(M[0])
@@ -174,15 +183,16 @@ class FlexOctBank:
 class OctCQT:
     """Invertible octave-mode CQT over one buffer (oracle).
 
-    Tables follow oct_cqt.py:36-82 (float32, bit-identical to the reference);
+    Tables follow oct_cqt.py:36-82 (in the bank's dtype: float32 by default,
+    bit-identical to the reference, or float64);
     fwd follows oct_cqt.py:84-96 and bwd oct_cqt.py:98-117, both evaluated in
     float64. Adjoints are derived from the real inner product (see the
     function docstrings); they are the gradients torch autograd produces
     through the reference transform.
     """
 
-    def __init__(self, num_octs, bins_per_oct, fs=44100, audio_len=44100):
-        self.bank = FlexOctBank(num_octs, bins_per_oct, fs, audio_len)
+    def __init__(self, num_octs, bins_per_oct, fs=44100, audio_len=44100, dtype=np.float32):
+        self.bank = FlexOctBank(num_octs, bins_per_oct, fs, audio_len, dtype=dtype)
         bank = self.bank
         self.Ls = audio_len
         self.nn = bank.nn
@@ -195,9 +205,9 @@ class OctCQT:
         def enc_dec_group(band_idx, Lo):
             nb = len(band_idx)
             idx = np.zeros((nb, Lo), dtype=np.int64)
-            gv = np.zeros((nb, Lo), dtype=np.float32)
+            gv = np.zeros((nb, Lo), dtype=dtype)
             pos = np.zeros((nb, Lo), dtype=np.int64)
-            gdv = np.zeros((nb, Lo), dtype=np.float32)
+            gdv = np.zeros((nb, Lo), dtype=dtype)
             for k, bi in enumerate(band_idx):
                 wr = bank.wins[bi]
                 Lg = wr.shape[0]
@@ -207,7 +217,7 @@ class OctCQT:
                 idx[k, Lo - l:] = wr[:l]
                 gv[k, :r] = gs[l:]
                 gv[k, Lo - l:] = gs[:l]
-                gd = bank.gd[bi] * np.float32(Lo)
+                gd = bank.gd[bi] * dtype(Lo)
                 gdv[k, :r] = gd[:r]
                 gdv[k, Lo - l:] = gd[r:]
                 pos[k, :r] = wr[l:]
@@ -215,7 +225,7 @@ class OctCQT:
             conj = idx > half
             idx = np.where(conj, nn - idx, idx)
             valid = pos <= half
-            gdv = (gdv * valid).astype(np.float32)
+            gdv = (gdv * valid).astype(dtype)
             pos = np.where(valid, pos, 0)
             return idx, gv, pos, gdv, conj
 

@@ -5,9 +5,9 @@ Runs ONCE, in the build container, on CPU:  python tests/golden/make_golden.py
 layouts (golden_layouts.npz, four further layouts).
 
 Why an import: the reference holds no golden vectors, and the bank numerics
-(np.round ties in filterbank.py:129-149, the mirrored block-size write one
-slot low at filterbank.py:165 that makes Mnyq 2048, the float32 frame
-diagonal of ref_util.py:46-55) and the SlicedCQT roll/overlap-add
+(np.round ties in filterbank.py:74-76 and 85-94, the mirrored block-size
+write one slot low at filterbank.py:110 that makes Mnyq 2048, the float32
+frame diagonal of ref_util.py:43-52) and the SlicedCQT roll/overlap-add
 conventions (sliced.py:106-167) are fixed by no closed form. So this script
 imports the reference's pure-torch modules from /root/reference and records
 their outputs on closed-form inputs. The reference never travels: only the

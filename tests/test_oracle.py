@@ -77,6 +77,53 @@ def test_dual_frame_identity(oracle):
     assert np.max(np.abs(acc - 1.0)) < 1e-6
 
 
+# ------------------------------------------------------- float64 bank
+
+@pytest.fixture(scope="module")
+def oracle64():
+    return co.OctCQT([3, 4, 2], [8, 16, 32], 44100, N, dtype=np.float64)
+
+
+def test_float64_bank_pins(oracle64, golden):
+    """The float64 bank (reference OctCQT(dtype=torch.float64): windows and
+    frame diagonal in float64, filterbank.py:114-117) is pinned three ways:
+    its windows round to the reference's float32 windows bit for bit (the
+    float32 bank is float32(float64 Hann)), its index tables are the
+    reference's, and its frame identity sum_i M_i g_i gd_i = 1 holds to
+    float64 rounding."""
+    b = oracle64.bank
+    kept = b.fbins + 2
+    g = np.concatenate([b.g[i] for i in range(kept)])
+    assert g.dtype == np.float64
+    assert np.array_equal(g.astype(np.float32).view(np.uint32), golden["bank_g_kept"].view(np.uint32))
+    ref = golden["group_table_sha256"].tolist()
+    got = group_hashes(oracle64.all_groups)
+    for r, h in zip(ref, got):
+        assert (h[0], h[2], h[4]) == (r[0], r[2], r[4])   # idx, pos, conj
+    acc = np.zeros(b.nn)
+    for gi, gd, m, rng in zip(b.g, b.gd, b.M, b.wins):
+        acc[rng] += float(m) * np.fft.fftshift(gi) * np.fft.fftshift(gd)
+    assert np.max(np.abs(acc - 1.0)) < 1e-13
+
+
+def test_float64_round_trip_exact(oracle64):
+    """A painless frame reconstructs exactly in exact arithmetic, so the
+    float64 bank's round trip reaches near machine precision (>= 250 dB);
+    the float32 bank stops near 147 dB even in float64 arithmetic."""
+    x, _ = inputs()
+    assert co.snr_db(x, oracle64.bwd(*oracle64.fwd(x))) >= 250
+
+
+def test_planted_float32_diagonal_fails_float64_bar(monkeypatch):
+    """The slip of accumulating a float64 bank's frame diagonal in float32
+    (float64 windows, float32 diagonal) must miss the float64 round-trip bar."""
+    orig = co.nsdual
+    monkeypatch.setattr(co, "nsdual", lambda g, wins, nn, M, dtype=np.float32: orig(g, wins, nn, M, np.float32))
+    planted = co.OctCQT([3, 4, 2], [8, 16, 32], 44100, N, dtype=np.float64)
+    x, _ = inputs()
+    assert co.snr_db(x, planted.bwd(*planted.fwd(x))) < 200
+
+
 # ------------------------------------------------------- forward / inverse
 
 def test_fwd_matches_reference(oracle, golden):
