@@ -395,15 +395,22 @@ def _cpu_baseline(port, cores, batch, budget_s, budget_b1_s, max_reps):
 # ---------------------------------------------------- single-launch path
 
 def single_launch(f, x, eager):
-    """The single-launch directions (one cooperative launch each, the
-    reference's persistent pair) at the batch of x, stream-launched back to
-    back, and whether they reproduce the six-launch round trip bit for bit."""
-    step = lambda: f.persist_inv(*f.persist_fwd(x))
+    """The single-launch directions (one launch of persistent workgroups per
+    direction, the reference's persistent pair) at the batch of x,
+    stream-launched back to back, and whether they reproduce the six-launch
+    round trip bit for bit. The timed calls skip the per-call error check
+    (a host synchronization); the error word is read once after them and a
+    nonzero word fails the bench."""
+    B = x.shape[0]
+    step = lambda: f.persist_inv(*f.persist_fwd(x, check=False), check=False)
     with torch.no_grad():
-        same = bool(torch.equal(step(), eager))
+        same = bool(torch.equal(f.persist_inv(*f.persist_fwd(x)), eager))
         ms = min(per_step_ms(step), per_step_ms(step))
-    return {"ms": ms, "round_trips_per_s": x.shape[0] / (ms * 1e-3), "equal_to_six_launch_bitwise": same,
-            "launch_mode": "stream launches", "launches_per_round_trip": 2}
+    err = f.sync_error(B)
+    if err:
+        raise RuntimeError(f"single-launch error word {err} at batch {B}")
+    return {"ms": ms, "round_trips_per_s": B / (ms * 1e-3), "equal_to_six_launch_bitwise": same,
+            "launch_mode": "stream launches", "launches_per_round_trip": 2, "error_word": err}
 
 
 def launch_floor(f, dev):
@@ -421,7 +428,7 @@ def launch_floor(f, dev):
 
 def single_launch_workload(f, dev):
     """--single-launch-only: both paths at batches 1, 16, 64 and the
-    per-launch floor, for a kernel trace of the cooperative kernels."""
+    per-launch floor, for a kernel trace of the single-launch kernels."""
     out = {"launch_floor": launch_floor(f, dev), "per_batch": {}}
     for B in (1, 16, 64):
         x = (torch.from_numpy(sinusoids()) if B == 1 else randn(B, 0)).to(dev)
@@ -434,6 +441,98 @@ def single_launch_workload(f, dev):
         out["per_batch"][str(B)] = r
         log(f"B={B}: six launches {six:.4f} ms, single launch per direction {r['ms']:.4f} ms "
             f"(bitwise equal: {r['equal_to_six_launch_bitwise']})")
+    return out
+
+
+def stage_trace_summary(tr, G, ntrace, nfields):
+    """Per-stage figures of one single-launch call's stage trace (the
+    fcqt_persist_trace records of its G workgroups): per stage the task
+    count, medians / 90th percentiles of claim-or-wait, body and count-in
+    times, when the stage's first task was ready and its last done; how
+    many task bodies of each stage run, and how many tasks wait after their
+    claim, in every 2 us of the call; and when each XCD's last task ended.
+    Times in us from the first workgroup's start (100 MHz clock)."""
+    a = tr.view(-1, ntrace, nfields)[:G].cpu().numpy().astype(np.int64)
+    start = a[:, ntrace - 1, 0]
+    t0 = start[start > 0].min()
+    rows = []
+    for w in range(G):
+        for i in range(ntrace - 1):
+            info = int(a[w, i, 0])
+            if info == 0:
+                break
+            rows.append((int(a[w, ntrace - 1, 1]), info & 0xff, a[w, i, 1] - t0, a[w, i, 2] - t0, a[w, i, 3] - t0,
+                         a[w, i, 4] - t0))
+    r = np.array(rows, dtype=np.int64)
+    us = lambda v: np.round(v / 100.0, 2)
+    out = {"workgroups": int(G), "tasks": len(r), "span_us": float(us(r[:, 5].max())), "stages": {}}
+    bins = np.arange(0, r[:, 5].max() + 200, 200)
+    for st in (1, 2, 3):
+        m = r[r[:, 1] == st]
+        if not len(m):
+            continue
+        cw, body, sig = m[:, 3] - m[:, 2], m[:, 4] - m[:, 3], m[:, 5] - m[:, 4]
+        out["stages"][str(st)] = {
+            "tasks": len(m),
+            "claim_or_wait_us": [float(us(np.median(cw))), float(us(np.percentile(cw, 90)))],
+            "body_us": [float(us(np.median(body))), float(us(np.percentile(body, 90)))],
+            "count_in_us": [float(us(np.median(sig))), float(us(np.percentile(sig, 90)))],
+            "first_ready_us": float(us(m[:, 3].min())), "last_done_us": float(us(m[:, 5].max())),
+            "running_per_2us": [int(np.sum((m[:, 3] <= t) & (m[:, 4] > t))) for t in bins],
+            "waiting_per_2us": [int(np.sum((m[:, 2] <= t) & (m[:, 3] > t))) for t in bins]}
+    out["xcd_end_us"] = [float(us(r[r[:, 0] == x][:, 5].max())) for x in range(8) if np.any(r[:, 0] == x)]
+    return out
+
+
+def single_launch_trace(dev, batches=(1, 16, 64)):
+    """--single-launch-trace: one call of each single-launch direction per
+    batch size through the trace build of the library
+    (libflashcqt_flowtrace.so), with its per-stage timeline; beside it the
+    time per call of the library's single-launch and three-launch
+    directions (stream-launched back to back, check=False)."""
+    from flash_cqt import OctCQT, _native
+    from flash_cqt.fused import FusedOctCQT
+    cqt_gpu = OctCQT([3, 4, 2], [8, 16, 32], fs=FS, audio_len=N, device=dev)
+    f = FusedOctCQT(cqt_gpu, dev)
+    ft = FusedOctCQT(cqt_gpu, dev)
+    ft.lib = _native.load_variant("flowtrace")
+    nt, nf = 32, 6
+    tr = torch.zeros(8 * 256 * nt * nf, dtype=torch.int64, device=dev)
+    _native.check(ft.lib.fcqt_persist_trace(tr.data_ptr(), tr.numel() * 8), "persist_trace")
+    out = {}
+    for B in batches:
+        x = (torch.from_numpy(sinusoids()) if B == 1 else randn(B, 0)).to(dev)
+        with torch.no_grad():
+            KR, KI = f.fwd(x)
+            k = torch.complex(KR, KI).clone()
+            y = f.bwd(KR, KI).clone()
+            r = {"ms_per_call": {
+                "single_launch_analysis": per_step_ms(lambda: f.persist_fwd(x, check=False)),
+                "three_launch_analysis": per_step_ms(lambda: f.fwd(x)),
+                "single_launch_synthesis": per_step_ms(lambda: f.persist_inv(KR, KI, check=False)),
+                "three_launch_synthesis": per_step_ms(lambda: f.bwd(KR, KI))}}
+            if f.sync_error(B):
+                raise RuntimeError(f"single-launch error word {f.sync_error(B)} at batch {B}")
+            for name, fn in (("analysis", lambda: ft.persist_fwd(x)), ("synthesis", lambda: ft.persist_inv(KR, KI))):
+                fn()
+                tr.zero_()
+                torch.cuda.synchronize()
+                res = fn()
+                torch.cuda.synchronize()
+                same = torch.equal(torch.complex(*res), k) if name == "analysis" else torch.equal(res, y)
+                G = int(np.count_nonzero(tr.view(-1, nt, nf)[:, nt - 1, 0].cpu().numpy()))
+                r[name] = stage_trace_summary(tr, G, nt, nf)
+                r[name]["equal_to_library_bitwise"] = bool(same)
+                st = r[name]["stages"]
+                log(f"B={B} {name}: span {r[name]['span_us']:.1f} us; " + "; ".join(
+                    f"stage {k_}: claim/wait {v['claim_or_wait_us'][0]:.2f} body {v['body_us'][0]:.2f} "
+                    f"ready {v['first_ready_us']:.1f}..done {v['last_done_us']:.1f} us" for k_, v in st.items()))
+        ms = r["ms_per_call"]
+        log(f"B={B}: per call single/three launches: analysis {ms['single_launch_analysis'] * 1e3:.1f} / "
+            f"{ms['three_launch_analysis'] * 1e3:.1f} us, synthesis {ms['single_launch_synthesis'] * 1e3:.1f} / "
+            f"{ms['three_launch_synthesis'] * 1e3:.1f} us")
+        out[str(B)] = r
+    _native.check(ft.lib.fcqt_persist_trace(None, 0), "persist_trace")
     return out
 
 
@@ -698,9 +797,12 @@ def main():
     ap.add_argument("--sliced-only", action="store_true")
     ap.add_argument("--sliced-long-only", action="store_true")
     ap.add_argument("--no-single-launch", action="store_true",
-                    help="skip the single-launch (cooperative) directions")
+                    help="skip the single-launch directions (one launch of persistent workgroups each)")
     ap.add_argument("--single-launch-only", action="store_true",
                     help="time only the single-launch directions and the per-launch floor; print their JSON")
+    ap.add_argument("--single-launch-trace", action="store_true",
+                    help="the single-launch directions' per-stage timeline (trace build of the library) at batches "
+                         "1, 16, 64; print its JSON")
     ap.add_argument("--band-tasks", type=int, default=None,
                     help="with --kernels-only: run only the band kernels, on the first K tasks")
     ap.add_argument("--lib-variant", choices=("xlane",), default=None,
@@ -727,6 +829,9 @@ def main():
         return
     if args.sliced_long_only:
         print(json.dumps(json_safe(sliced_long(dev))), flush=True)
+        return
+    if args.single_launch_trace:
+        print(json.dumps(json_safe(single_launch_trace(dev))), flush=True)
         return
     cqt_gpu = OctCQT([3, 4, 2], [8, 16, 32], fs=FS, audio_len=N, device=dev)
     f = FusedOctCQT(cqt_gpu, dev)

@@ -2,10 +2,11 @@
 
     python flash-cqt_amd/build.py [--verbose]
 
-Output: flash-cqt_amd/flash_cqt/_lib/libflashcqt.so, and beside it the
-variant library libflashcqt_xlane.so (the same sources with the band units of
+Output: flash-cqt_amd/flash_cqt/_lib/libflashcqt.so, and beside it two
+variant libraries of the same sources: libflashcqt_xlane.so (the band units of
 M <= 256 exchanging across lanes instead of through LDS; the benchmark and the
-GPU tests compare the two). Both compile in parallel. Flags: -O3 for gfx950,
+GPU tests compare the two) and libflashcqt_flowtrace.so (the single-launch
+kernels stamping a stage trace, fcqt_persist_trace). All compile in parallel. Flags: -O3 for gfx950,
 packed fp32 instructions disabled (-Xclang -target-feature -Xclang
 -packed-fp32-ops). The host pass warns that it does not know the packed-fp32
 feature; that warning is harmless.
@@ -37,7 +38,8 @@ def hipcc():
 
 
 # variant name -> (output, extra defines)
-VARIANTS = {"": (OUT, ()), "xlane": (OUT.with_name("libflashcqt_xlane.so"), ("-DFCQT_XLANE_MAX_M=256",))}
+VARIANTS = {"": (OUT, ()), "xlane": (OUT.with_name("libflashcqt_xlane.so"), ("-DFCQT_XLANE_MAX_M=256",)),
+            "flowtrace": (OUT.with_name("libflashcqt_flowtrace.so"), ("-DFCQT_FLOW_TRACE",))}
 
 
 def command(out=OUT, defines=()):

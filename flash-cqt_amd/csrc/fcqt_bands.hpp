@@ -92,8 +92,8 @@ __device__ __forceinline__ void store_coef(float* __restrict__ cre, float* __res
 }
 
 // This thread's 16 records of its task (kernel order).
-__device__ __forceinline__ void load_records(int2* rv, const int2* __restrict__ rec, int task) {
-    const int2* rr = rec + (long)task * kBandPoints + threadIdx.x;
+__device__ __forceinline__ void load_records(int2* rv, const int2* __restrict__ rec, int task, int tid) {
+    const int2* rr = rec + (long)task * kBandPoints + tid;
 #pragma unroll
     for (int s = 0; s < 16; ++s) rv[s] = rr[s * kBandThreads];
 }
@@ -107,12 +107,13 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
                                            const int2* rv, const float2* __restrict__ xb,
                                            float* __restrict__ cre, float* __restrict__ cim,
                                            const long ncoef, const SliceMap sm,
-                                           const float2* __restrict__ tws, float2* lds, float2* tw2) {
+                                           const float2* __restrict__ tws, float2* lds, float2* tw2,
+                                           const int tid) {
     using P = Plan<M>;
-    const int u = threadIdx.x / P::T;
-    const int t = threadIdx.x - u * P::T;
+    const int u = tid / P::T;
+    const int t = tid - u * P::T;
     Tw2Copy<M, kBandThreads> c2;
-    fetch_tw2<M, kBandThreads>(c2, tws, threadIdx.x);
+    fetch_tw2<M, kBandThreads>(c2, tws, tid);
     Tw3<M> w3;
     load_tw3<M>(w3, tws, t);
     // v = w X[k], conjugated for taps past Nyquist: the record's weight
@@ -125,7 +126,7 @@ __device__ __forceinline__ void route_band(const int4 task, const int task_id, c
         const float w = __int_as_float(rv[r].y);
         v[r] = make_float2(fabsf(w) * x.x, w * x.y);
     }
-    put_tw2<M, kBandThreads>(tw2, c2, threadIdx.x);
+    put_tw2<M, kBandThreads>(tw2, c2, tid);
     band_fft<M, +1>(v, lds + u * P::US, t, tw2, w3);
     if (u < task.z) {
         long ob;
@@ -147,10 +148,11 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
                                              const int2* __restrict__ scat, const float* __restrict__ cre,
                                              const float* __restrict__ cim, float* __restrict__ f,
                                              const long ncoef, const SliceMap sm,
-                                             const float2* __restrict__ tws, float2* lds, float2* tw2) {
+                                             const float2* __restrict__ tws, float2* lds, float2* tw2,
+                                             const int tid) {
     using P = Plan<M>;
-    const int u = threadIdx.x / P::T;
-    const int t = threadIdx.x - u * P::T;
+    const int u = tid / P::T;
+    const int t = tid - u * P::T;
     const bool active = u < task.z;
     // coefficients first, then the twiddles, then the records (needed only
     // after the transform)
@@ -163,12 +165,12 @@ __device__ __forceinline__ void scatter_band(const int4 task, const int task_id,
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = load_coef<LAYOUT>(cr, ci, (t + P::T * r + shift) & (M - 1));
     Tw2Copy<M, kBandThreads> c2;
-    fetch_tw2<M, kBandThreads>(c2, tws, threadIdx.x);
+    fetch_tw2<M, kBandThreads>(c2, tws, tid);
     Tw3<M> w3;
     load_tw3<M>(w3, tws, t);
     int2 rv[16];
-    load_records(rv, scat, task_id);
-    put_tw2<M, kBandThreads>(tw2, c2, threadIdx.x);
+    load_records(rv, scat, task_id, tid);
+    put_tw2<M, kBandThreads>(tw2, c2, tid);
     band_fft<M, -1>(v, lds + u * P::US, t, tw2, w3);
     if (active) {
         float2* fb = reinterpret_cast<float2*>(f) + (long)b * kFRow;
@@ -210,16 +212,17 @@ __device__ __forceinline__ void route_task(const int task_id, const int b, const
                                            float* __restrict__ cre, float* __restrict__ cim,
                                            const int2* __restrict__ rec, const int4* __restrict__ tasks,
                                            const long ncoef, const SliceMap& sm,
-                                           const float2* __restrict__ tws, float2* lds) {
+                                           const float2* __restrict__ tws, float2* lds,
+                                           const int tid = threadIdx.x) {
     float2* tw2 = lds + kBandLds;
     // the records issue first (they need the task index only); the task
     // record then selects the band length, and the gathers follow inside
     int2 rv[16];
-    load_records(rv, rec, task_id);
+    load_records(rv, rec, task_id, tid);
     const float2* xb = xs + (long)b * kXStride;
     const int4 td = tasks[task_id];
     if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
-#define FCQT_ROUTE(M_) route_band<M_, LAYOUT, WT>(td, task_id, b, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2)
+#define FCQT_ROUTE(M_) route_band<M_, LAYOUT, WT>(td, task_id, b, rv, xb, cre, cim, ncoef, sm, tws, lds, tw2, tid)
     switch (td.x) {
         case 32: FCQT_ROUTE(32); break;
         case 64: FCQT_ROUTE(64); break;
@@ -241,11 +244,12 @@ __device__ __forceinline__ void scatter_task(const int task_id, const int b, con
                                              const float* __restrict__ cim, float* __restrict__ f,
                                              const int2* __restrict__ scat, const int4* __restrict__ tasks,
                                              const long ncoef, const SliceMap& sm,
-                                             const float2* __restrict__ tws, float2* lds) {
+                                             const float2* __restrict__ tws, float2* lds,
+                                             const int tid = threadIdx.x) {
     float2* tw2 = lds + kBandLds;
     const int4 td = tasks[task_id];
     if (td.y < 0 || (long)td.y + (long)td.z * td.x > ncoef) return;   // task outside the coefficient row
-#define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT, WT>(td, task_id, b, scat, cre, cim, f, ncoef, sm, tws, lds, tw2)
+#define FCQT_SCATTER(M_) scatter_band<M_, LAYOUT, WT>(td, task_id, b, scat, cre, cim, f, ncoef, sm, tws, lds, tw2, tid)
     switch (td.x) {
         case 32: FCQT_SCATTER(32); break;
         case 64: FCQT_SCATTER(64); break;

@@ -129,11 +129,12 @@ constexpr int row_lds() { return RPW * Plan<256>::US + tw2_len<256>(); }
 template <bool SLICED, int CPW>
 __device__ __forceinline__ void col_fwd_tile(const int b, const int cg, const float2* __restrict__ in,
                                              float2* __restrict__ out, const float2* __restrict__ twp,
-                                             const float2* __restrict__ tws, const SliceSrc& src, float2* lds) {
+                                             const float2* __restrict__ tws, const SliceSrc& src, float2* lds,
+                                             const int tid = threadIdx.x) {
     using P = Plan<128>;
     float2* tw2 = lds + CPW * P::US;
-    const int c = threadIdx.x & (CPW - 1);        // column within the tile
-    const int t = threadIdx.x / CPW;              // thread within the column FFT, < 8
+    const int c = tid & (CPW - 1);                // column within the tile
+    const int t = tid / CPW;                      // thread within the column FFT, < 8
     const int n2 = cg * CPW + c;
     float2 v[16];
     if constexpr (SLICED) {
@@ -158,7 +159,7 @@ __device__ __forceinline__ void col_fwd_tile(const int b, const int cg, const fl
         for (int r = 0; r < 16; ++r) v[r] = xb[256 * (t + 8 * r) + n2];
     }
     // every twiddle this thread needs, in flight with the data
-    load_tw2_lds<128>(tw2, tws, threadIdx.x, 8 * CPW);
+    load_tw2_lds<128>(tw2, tws, tid, 8 * CPW);
     // W_L^{n2 k1}, k1 = t + 8 q + 16 r, from the rows t, 8 and 16 r of the
     // table: W^{n2 t} W^{8 n2 q} W^{16 n2 r} (two roundings more than a table value)
     float2 tb = twp[t * 256 + n2], t8 = twp[8 * 256 + n2];
@@ -203,7 +204,8 @@ template <int CPW, bool WT>
 __device__ __forceinline__ void col_inv_tile(const int b, const int w, const float2* __restrict__ f,
                                              float2* __restrict__ out, const float2* __restrict__ twp,
                                              const float2* __restrict__ twn, const int* __restrict__ fold,
-                                             const float2* __restrict__ tws, float2* lds) {
+                                             const float2* __restrict__ tws, float2* lds,
+                                             const int tid = threadIdx.x) {
     using P = Plan<128>;
     constexpr int H = CPW / 2;                    // column pairs per workgroup
     constexpr int kWgs = 256 / CPW;               // workgroups per slice
@@ -213,8 +215,8 @@ __device__ __forceinline__ void col_inv_tile(const int b, const int w, const flo
     static_assert(kShare * kFoldLists == kWgs && kEnt * kThreads == kFoldPerWg, "fold list split");
     // lds: staged bins, then the FFT exchange; then the twiddle block
     float2* tw2 = lds + CPW * P::US;
-    const int c = threadIdx.x & (CPW - 1);
-    const int t = threadIdx.x / CPW;
+    const int c = tid & (CPW - 1);
+    const int t = tid / CPW;
     const int col = inv_col<CPW>(w, c);
     const float2* fb = f + (long)b * kFRow;
     float2* raw = lds + c * P::US;
@@ -222,7 +224,7 @@ __device__ __forceinline__ void col_inv_tile(const int b, const int w, const flo
     // from the list of the wide workgroup that contains this one
     int ent[kEnt];
 #pragma unroll
-    for (int e = 0; e < kEnt; ++e) ent[e] = fold[(w / kShare) * kFoldPerWg + threadIdx.x + e * kThreads];
+    for (int e = 0; e < kEnt; ++e) ent[e] = fold[(w / kShare) * kFoldPerWg + tid + e * kThreads];
     float2 q0[16], q1[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -236,7 +238,7 @@ __device__ __forceinline__ void col_inv_tile(const int b, const int w, const flo
     float2 tn[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) tn[r] = twn[2048 * r];
-    load_tw2_lds<128>(tw2, tws, threadIdx.x, kThreads);
+    load_tw2_lds<128>(tw2, tws, tid, kThreads);
     // overflow slot sums of this workgroup's listed bins and their LDS
     // positions (bin L is parked in column 0's pad slot, raw[128] of slot 0)
     float2 oadd[kEnt];
@@ -343,12 +345,12 @@ __device__ __forceinline__ int fwd_row(int w, int rho) {
 template <bool HOLD>
 __device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, float2* lds, float2* tw2,
                                                int rho, int t, int nthreads, const float2* __restrict__ tws,
-                                               float2* vhold, float2* shold) {
+                                               float2* vhold, float2* shold, const int tid) {
     using P = Plan<256>;
     float2 v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) v[r] = yrow[t + 16 * r];
-    load_tw2_lds<256>(tw2, tws, threadIdx.x, nthreads);
+    load_tw2_lds<256>(tw2, tws, tid, nthreads);
     if constexpr (HOLD) {
         asm volatile("" : "+v"(vhold->x), "+v"(vhold->y));
 #pragma unroll
@@ -371,23 +373,24 @@ __device__ __forceinline__ void row_fft_to_lds(const float2* __restrict__ yrow, 
 template <int RPW>
 __device__ __forceinline__ void row_fwd_tile(const int b, const int w, const float2* __restrict__ in,
                                              float2* __restrict__ xs, const float2* __restrict__ twn,
-                                             const float2* __restrict__ tws, float2* lds) {
+                                             const float2* __restrict__ tws, float2* lds,
+                                             const int tid = threadIdx.x) {
     using P = Plan<256>;
     float2* tw2 = lds + RPW * P::US;
-    const int rho = threadIdx.x >> 4;
-    const int t = threadIdx.x & 15;
+    const int rho = tid >> 4;
+    const int t = tid & 15;
     // untangle twiddles of this thread's output bins, loaded up front:
     // W_N^{k1 + 128 (kg + 16 u)} = W_N^{k1 + 128 kg} W_N^{2048 u}, the second
     // factor the same for the whole workgroup (one rounding more than a table value)
-    const int rho2 = threadIdx.x & (RPW - 1);     // output lanes walk the tile's rows
-    const int kg = threadIdx.x / RPW;             // < 16
+    const int rho2 = tid & (RPW - 1);             // output lanes walk the tile's rows
+    const int kg = tid / RPW;                     // < 16
     const int k1 = fwd_row<RPW>(w, rho2);
     float2 wb = twn[k1 + 128 * kg];
     float2 wu[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) wu[u] = twn[2048 * u];
     row_fft_to_lds<true>(in + (long)b * kL + (long)fwd_row<RPW>(w, rho) * 256, lds, tw2, rho, t, 16 * RPW, tws,
-                         &wb, wu);
+                         &wb, wu, tid);
     // untangle: lanes walk the tile's rows for coalesced stores
     const float2* s = lds + rho2 * P::US;
     // mirror bin L - k: row 128 - k1 at column 255 - k2; rows 0 and 64 are
@@ -407,7 +410,7 @@ __device__ __forceinline__ void row_fwd_tile(const int b, const int w, const flo
         xb[k1 + 128 * k2] = make_float2(0.5f * fmaf(wn.x, d.y, fmaf(wn.y, d.x, sm.x)),
                                         0.5f * fmaf(wn.y, d.y, fmaf(-wn.x, d.x, sm.y)));
     }
-    if (w == 0 && threadIdx.x == 0) {               // Nyquist bin from Z[0] (row 0, k2 = 0)
+    if (w == 0 && tid == 0) {                       // Nyquist bin from Z[0] (row 0, k2 = 0)
         const float2 z0 = lds[pad16(0)];
         xb[kL] = make_float2(z0.x - z0.y, 0.0f);
     }
@@ -416,15 +419,16 @@ __device__ __forceinline__ void row_fwd_tile(const int b, const int w, const flo
 
 template <int RPW, bool WT>
 __device__ __forceinline__ void row_inv_tile(const int b, const int rg, const float2* __restrict__ in,
-                                             float2* __restrict__ y, const float2* __restrict__ tws, float2* lds) {
+                                             float2* __restrict__ y, const float2* __restrict__ tws, float2* lds,
+                                             const int tid = threadIdx.x) {
     using P = Plan<256>;
     float2* tw2 = lds + RPW * P::US;
-    const int rho = threadIdx.x >> 4;
-    const int t = threadIdx.x & 15;
+    const int rho = tid >> 4;
+    const int t = tid & 15;
     row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * RPW + rho) * 256, lds, tw2, rho, t, 16 * RPW, tws,
-                          nullptr, nullptr);
-    const int rho2 = threadIdx.x & (RPW - 1);
-    const int kg = threadIdx.x / RPW;
+                          nullptr, nullptr, tid);
+    const int rho2 = tid & (RPW - 1);
+    const int kg = tid / RPW;
     const float2* s2 = lds + rho2 * P::US;
     const int kk1 = rg * RPW + rho2;
     constexpr float sc = 0.5f / (float)kL;     // 1/L of the inverse, 1/2 of the retangle
@@ -452,15 +456,15 @@ template <int RPW, bool ODD, bool PAIR>
 __device__ __forceinline__ void row_inv_ola_tile(const int b, const int rg, const int s, const int S,
                                                  const long length, const float2* __restrict__ in,
                                                  float* __restrict__ orow, const float2* __restrict__ tws,
-                                                 float2* lds) {
+                                                 float2* lds, const int tid = threadIdx.x) {
     using P = Plan<256>;
     float2* tw2 = lds + RPW * P::US;
-    const int rho = threadIdx.x >> 4;
-    const int t = threadIdx.x & 15;
+    const int rho = tid >> 4;
+    const int t = tid & 15;
     row_fft_to_lds<false>(in + (long)b * kL + (long)(rg * RPW + rho) * 256, lds, tw2, rho, t, 16 * RPW, tws,
-                          nullptr, nullptr);
-    const int rho2 = threadIdx.x & (RPW - 1);
-    const int kg = threadIdx.x / RPW;
+                          nullptr, nullptr, tid);
+    const int rho2 = tid & (RPW - 1);
+    const int kg = tid / RPW;
     const float2* s2 = lds + rho2 * P::US;
     const int kk1 = rg * RPW + rho2;
     constexpr float sc = 0.5f / (float)kL;     // 1/L of the inverse, 1/2 of the retangle

@@ -180,6 +180,6 @@ extern "C" int fcqt_workspace_sizes(const fcqt_tables* tab, int64_t batch, fcqt_
     out->scatter = batch * (int64_t)kFRow * 8;
     out->coef_plane = batch * tab->ncoef * 4;
     out->tail = batch * (int64_t)(kN / 2) * 4;
-    out->sync = (batch + 1) * (int64_t)FCQT_SYNC_PER_SLICE * 4;
+    out->sync = FCQT_SYNC_WORDS(batch) * 4;
     return FCQT_OK;
 }

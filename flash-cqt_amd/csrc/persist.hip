@@ -1,5 +1,6 @@
-// Single-launch directions: each direction of the round trip as one
-// ordinary launch whose stages wait for each other slice by slice.
+// Single-launch directions: each direction of the round trip as one launch
+// of persistent workgroups that take the direction's tasks from per-XCD
+// queues.
 //   analysis   stage 1: column tiles    stage 2: row tiles (untangle)
 //              stage 3: band route tasks
 //   synthesis  stage 1: band scatter tasks    stage 2: inverse column tiles
@@ -10,36 +11,37 @@
 // shapes whose per-slice arithmetic equals the other shapes'), so the results
 // equal the six-launch path bit for bit.
 //
-// Placement and waits. The hardware hands workgroup i to XCD i mod 8 (on
-// every partitioning of the chip, workgroups with equal blockIdx mod 8 share
-// an XCD and so an L2), and each XCD starts its workgroups in blockIdx order.
-// The grid gives all of a slice's workgroups one residue mod 8 and lays out
-// each XCD's share as [stage 1 of its slices][stage 2][stage 3]. A stage-2 or
-// stage-3 workgroup waits (one lane polls, with sleeps) until its slice's
-// previous stage has counted in. The workgroups it waits for started before
-// it on the same XCD and wait only on earlier stages, so every wait ends.
-// Producer and consumer share an L2, so a wait needs no L2 write-back: the
-// producer's stores are in the L2 when its counter moves (each lane waits for
-// its stores before the workgroup barrier), and the consumer drops its L1
-// before reading. Each stage-1 workgroup marks its XCD in the slice's record
-// and each waiting workgroup compares that mark with its own XCD; a mismatch,
-// or a wait that outlasts its bound (about two seconds), sets the error word,
-// so a broken placement assumption gives an error, never a hang or a silent
-// stale read. The last workgroup of a slice's last stage returns the slice's
-// record to zero, so the counters are ready for the next call (and for graph
-// replays) without a memset.
+// Queues and order. Queue x holds the slices x, x + 8, x + 16, ... and is
+// served only by workgroups that run on XCD x, read from the hardware
+// (HW_REG_XCC_ID), so the producer and the consumer of every intermediate
+// (W, X; F, W) share one L2 whatever the dispatcher's placement. A
+// workgroup takes the next position of its XCD's queue with one atomic
+// add; fcqt_flow.hpp maps positions to tasks in a slice-interleaved order
+// with lags d1 (stage 2 after stage 1) and d2 (stage 3 after stage 1), so
+// a task's dependencies were taken earlier, by running workgroups: every
+// wait ends, with any number of workgroups resident. A stage-2 or stage-3
+// task waits (one lane polls its slice's counter, with sleeps) for its
+// slice's previous stage; the producer's stores reach the shared L2 before
+// its counter moves (each lane waits for its stores before the workgroup
+// barrier), and the consumer drops its L1 before reading.
 //
-// Measured on MI355X (graphs of 20 calls), against the three launches of the
-// same direction: analysis 13.1 / 18.8 / 41.3 / 58.0 us against 11.5 / 17.0 /
-// 37.2 / 59.7 us at B = 1 / 16 / 64 / 128; synthesis 15.4 / 28.6 / 50.0 / 72.7
-// us against 13.5 / 18.6 / 39.0 / 80.2 us. The cooperative form with two
-// grid-wide barriers per direction took 231 / 250 us per direction at B = 64.
+// Failures become an error word, never a hang or a silent result: a wait
+// bounded by the chip's 100 MHz clock (two seconds) sets bit 1 and every
+// other wait then stops; the last workgroup to leave sets bit 4 if a queue
+// with tasks was never served (no workgroup ran on that XCD). Only when the
+// word is zero does that last workgroup return the counters to zero, so a
+// stale count can never satisfy a later call's wait; after a nonzero word
+// the caller synchronises and zero-fills the whole sync buffer.
+//
 // Reference semantics: fwd2_kernel / inv2_kernel, persist2.cu:140-222 (one
 // launch per direction; the reference's inverse also zeroes its atomic
 // scatter target first, which this engine's slot scatter does not need).
 #include "fcqt_passes.hpp"
 #include "fcqt_bands.hpp"
+#include "fcqt_flow.hpp"
 #include "fcqt_abi_internal.hpp"
+
+#include <algorithm>
 
 namespace fcqt {
 
@@ -56,12 +58,16 @@ static_assert(8 * kFColsPerTile == kFlowThreads && 16 * kFRowsPerTile == kFlowTh
 constexpr int kFlowLds = cmax(cmax(col_lds<kFColsPerTile>(), col_lds<kFInvColsPerTile>()),
                               cmax(row_lds<kFRowsPerTile>(), kBandTaskLds));
 
-// A slice's record: FCQT_SYNC_PER_SLICE words; the three stage counters and
-// the XCD mask each sit on their own 64-byte line.
-constexpr int kSyncStage1 = 0, kSyncStage2 = 16, kSyncStage3 = 32, kSyncXcd = 48;
-static_assert(FCQT_SYNC_PER_SLICE == 64, "slice record layout");
-constexpr int kWaitPolls = 1 << 22;    // polls of ~1000 cycles of sleep each: about two seconds
-constexpr int kXcds = 8;
+// sync buffer: per slice FCQT_SYNC_PER_SLICE words (stage-1 and stage-2
+// done counts, each on its own 128-byte line), then the head block of
+// FCQT_SYNC_HEAD_WORDS: error word, exit count, one claim counter per queue
+// (each on its own 128-byte line).
+constexpr int kSyncStage1 = 0, kSyncStage2 = 32;
+constexpr int kHeadError = 0, kHeadExit = 32, kHeadClaim = 64;
+static_assert(FCQT_SYNC_PER_SLICE == 64 && FCQT_SYNC_HEAD_WORDS == kHeadClaim + 32 * kFlowQueues,
+              "sync buffer layout");
+constexpr int64_t kWaitTicksDefault = 200000000;   // two seconds of the 100 MHz clock
+constexpr unsigned kErrTimeout = 1u, kErrUnserved = 4u;
 
 __device__ __forceinline__ unsigned xcc_id() {
     return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11)) & 15u;   // HW_REG_XCC_ID
@@ -89,139 +95,303 @@ struct FlowArgs {
     long ncoef;
     int ntasks;
     int batch;
+    FlowOrder order;
+    uint64_t wait_ticks;      // bound of a stage wait (100 MHz ticks)
+#ifdef FCQT_FLOW_TRACE
+    unsigned long long* trace;   // fcqt_persist_trace buffer, or null
+#endif
 };
 
-// This workgroup's stage (1, 2 or 3; 0 past its XCD's share), slice b and
-// index t within the stage, for stages of n1, n2, n3 workgroups per slice.
-__device__ __forceinline__ int flow_place(int n1, int n2, int n3, int batch, int& b, int& t) {
-    const int xcd = (int)(blockIdx.x % kXcds), i = (int)(blockIdx.x / kXcds);
-    const int nsl = batch > xcd ? (batch - xcd + kXcds - 1) / kXcds : 0;    // slices xcd, xcd + 8, ...
-    int stage, k;
-    if (i < nsl * n1) {
-        stage = 1, k = i;
-    } else if (i < nsl * (n1 + n2)) {
-        stage = 2, k = i - nsl * n1;
-    } else if (i < nsl * (n1 + n2 + n3)) {
-        stage = 3, k = i - nsl * (n1 + n2);
-    } else {
-        return 0;
+// Stage trace of the trace build (libflashcqt_flowtrace.so, built with
+// FCQT_FLOW_TRACE): lane 0 of each workgroup stamps the chip's 100 MHz
+// clock into FCQT_TRACE_TASKS records of FCQT_TRACE_FIELDS uint64 per
+// workgroup (blockIdx order). Record i < FCQT_TRACE_TASKS - 1 is the
+// workgroup's task i: {stage | slice << 8 | tile << 40, before its claim or
+// wait, task ready, body done, counted in}; the last record is {start, XCD,
+// left}. The library build records nothing (no code, no cost).
+constexpr int kTraceTasks = FCQT_TRACE_TASKS, kTraceFields = FCQT_TRACE_FIELDS;
+#ifdef FCQT_FLOW_TRACE
+static unsigned long long* g_trace = nullptr;
+__device__ __forceinline__ void trace_at(const FlowArgs& p, int i, int f, unsigned long long v) {
+    if (p.trace && threadIdx.x == 0 && i < kTraceTasks)
+        p.trace[((long)blockIdx.x * kTraceTasks + i) * kTraceFields + f] = v;
+}
+#else
+__device__ __forceinline__ void trace_at(const FlowArgs&, int, int, unsigned long long) {}
+#endif
+__device__ __forceinline__ unsigned long long clock100() { return __builtin_amdgcn_s_memrealtime(); }
+
+// One lane waits until *c >= target. False when the wait gave up: it ran
+// past its bound (error bit set here) or another wait had already failed.
+// The error word, one line that every waiting workgroup of the chip would
+// read, is looked at only once a wait has lasted kErrPollTicks.
+constexpr uint64_t kErrPollTicks = 2000;    // 20 us
+__device__ __forceinline__ bool flow_wait(const unsigned* c, unsigned target, unsigned* err, uint64_t bound) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        if (sync_load(c) >= target) return true;
+        const uint64_t dt = __builtin_amdgcn_s_memrealtime() - t0;
+        if (dt > bound) {
+            __hip_atomic_fetch_or(err, kErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        if (dt > kErrPollTicks && sync_load(err)) return false;
+        __builtin_amdgcn_s_sleep(4);
     }
-    const int n = stage == 1 ? n1 : (stage == 2 ? n2 : n3);
-    const int j = k / n;
-    t = k - j * n;
-    b = xcd + kXcds * j;
+}
+
+// Lane 0 takes the next position of this XCD's queue and waits for its
+// dependencies; the task (stage 0: the queue is done) goes to every lane
+// through LDS. A stage-2/3 task drops this CU's L1 before its body reads.
+// The claim is taken one task ahead: lane 0 issues the atomic for the
+// position after this one before the body starts, and reads it here at the
+// next task (`next`, -1 before the first), so its latency (about as long as
+// a load round trip) hides under the body's own loads. A workgroup thus
+// holds its next position while it runs a task; every dependency of that
+// position still sits at an earlier one, so every wait still ends.
+__device__ __forceinline__ int flow_next(const FlowArgs& p, int x, long K, int* sh, long& b, int& t, long& next) {
+    unsigned* head = p.sync + (long)p.batch * FCQT_SYNC_PER_SLICE;
+    unsigned* claim = head + kHeadClaim + 32 * x;
+    if (threadIdx.x == 0) {
+        const long j = next >= 0 ? next
+                                 : (long)__hip_atomic_fetch_add(claim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int stage = 0, tt = 0;
+        long k = 0;
+        const long end = flow_end(p.order, K);
+        if (j < end) {
+            flow_decode(p.order, K, j, stage, k, tt);
+            const long g = x + (long)kFlowQueues * k;
+            const unsigned* rec = p.sync + g * FCQT_SYNC_PER_SLICE;
+            if (stage == 2) flow_wait(rec + kSyncStage1, (unsigned)p.order.n1, head + kHeadError, p.wait_ticks);
+            if (stage == 3) flow_wait(rec + kSyncStage2, (unsigned)p.order.n2, head + kHeadError, p.wait_ticks);
+            sh[1] = (int)g;
+            sh[2] = tt;
+            // the position after this one, in flight during the body
+            next = (long)__hip_atomic_fetch_add(claim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        sh[0] = stage;
+    }
+    __syncthreads();
+    // workgroup-uniform: scalar registers, as blockIdx-derived indices would be
+    const int stage = __builtin_amdgcn_readfirstlane(sh[0]);
+    b = __builtin_amdgcn_readfirstlane(sh[1]);
+    t = __builtin_amdgcn_readfirstlane(sh[2]);
+    if (stage >= 2) asm volatile("buffer_inv sc0" ::: "memory");
     return stage;
 }
 
 // After a stage-1 or stage-2 body: this workgroup's stores are in the L2,
-// then the slice's counter moves (stage 1 also marks its XCD).
-__device__ __forceinline__ void flow_signal(unsigned* rec, int counter, bool mark_xcd) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// then the slice's counter moves. After a stage-3 body: a barrier (the next
+// task reuses the LDS).
+__device__ __forceinline__ void flow_done(const FlowArgs& p, int stage, long b) {
+    if (stage < 3) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
-        if (mark_xcd)
-            __hip_atomic_fetch_or(rec + kSyncXcd, 1u << xcc_id(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_fetch_add(rec + counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (stage < 3 && threadIdx.x == 0)
+        __hip_atomic_fetch_add(p.sync + b * FCQT_SYNC_PER_SLICE + (stage == 1 ? kSyncStage1 : kSyncStage2), 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Before a stage-2 or stage-3 body: wait until `target` workgroups of the
-// slice's previous stage have counted in, check that they ran on this XCD,
-// then drop this CU's L1 lines (the data comes from the shared L2).
-__device__ __forceinline__ void flow_wait(unsigned* rec, int counter, unsigned target, unsigned* err) {
+// A workgroup leaving: the last one checks that every queue with tasks was
+// served and, if the error word is zero, returns every counter to zero.
+__device__ __forceinline__ void flow_exit(const FlowArgs& p, int* sh) {
+    unsigned* head = p.sync + (long)p.batch * FCQT_SYNC_PER_SLICE;
     if (threadIdx.x == 0) {
-        int n = 0;
-        while (sync_load(rec + counter) < target) {
-            __builtin_amdgcn_s_sleep(16);
-            if (++n > kWaitPolls) {
-                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const unsigned left = __hip_atomic_fetch_add(head + kHeadExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int clear = 0;
+        if (left == gridDim.x - 1) {
+            unsigned unserved = 0;
+            for (int q = 0; q < kFlowQueues; ++q)
+                if ((long)sync_load(head + kHeadClaim + 32 * q) < flow_end(p.order, flow_slices(p.batch, q)))
+                    unserved = 1;
+            if (unserved)
+                __hip_atomic_fetch_or(head + kHeadError, kErrUnserved, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            clear = sync_load(head + kHeadError) == 0u;
         }
-        if (sync_load(rec + kSyncXcd) != (1u << xcc_id()))
-            __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh[3] = clear;
     }
     __syncthreads();
-    asm volatile("buffer_inv sc0" ::: "memory");
-}
-
-// After a stage-3 body: the slice's last workgroup clears its record.
-__device__ __forceinline__ void flow_finish(unsigned* rec, unsigned n3) {
-    __syncthreads();
-    if (threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(rec + kSyncStage3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n3 - 1) {
-        __hip_atomic_store(rec + kSyncStage1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(rec + kSyncStage2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(rec + kSyncXcd, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(rec + kSyncStage3, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (sh[3]) {
+        for (long g = threadIdx.x; g < p.batch; g += kFlowThreads) {
+            __hip_atomic_store(p.sync + g * FCQT_SYNC_PER_SLICE + kSyncStage1, 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.sync + g * FCQT_SYNC_PER_SLICE + kSyncStage2, 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (threadIdx.x < kFlowQueues)
+            __hip_atomic_store(head + kHeadClaim + 32 * threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0)
+            __hip_atomic_store(head + kHeadExit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-template <int LAYOUT>
-__global__ __launch_bounds__(kFlowThreads) void k_flow_analysis(const FlowArgs p) {
+// The thread index and the table pointers of one task, made opaque to the
+// compiler at every task. Seen as loop invariants, the bodies' thread-index
+// address arithmetic (all seven band lengths, both pass shapes) and their
+// table loads are hoisted out of the task loop and kept live across it:
+// 255-256 VGPRs, a quarter of the occupancy. Recomputed per task they cost
+// a few instructions.
+template <class T>
+__device__ __forceinline__ T* opaque(T* q) {
+    asm volatile("" : "+s"(q));
+    return q;
+}
+
+__device__ __forceinline__ FlowArgs flow_task_args(const FlowArgs& p, int& tid) {
+    tid = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    FlowArgs q = p;
+    q.twp = opaque(p.twp);
+    q.twh = opaque(p.twh);
+    q.tws = opaque(p.tws);
+    q.tasks = opaque(p.tasks);
+    q.rec = opaque(p.rec);
+    q.ovf = opaque(p.ovf);
+    return q;
+}
+
+template <int LAYOUT, bool WT>
+__global__ __launch_bounds__(kFlowThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_flow_analysis(const FlowArgs p) {
     __shared__ float2 lds[kFlowLds];
-    int b = 0, t = 0;
-    const int stage = flow_place(kFColTiles, kFRowTiles, p.ntasks, p.batch, b, t);
-    if (stage == 0) return;
-    unsigned* rec = p.sync + (long)b * FCQT_SYNC_PER_SLICE;
-    unsigned* err = p.sync + (long)p.batch * FCQT_SYNC_PER_SLICE;
-    if (stage == 1) {
-        col_fwd_tile<false, kFColsPerTile>(b, t, p.x, p.work, p.twp, p.tws, SliceSrc{nullptr, nullptr, 1, 1, 0, 0, 0, nullptr, 1, 1, 1},
-                                           lds);
-        flow_signal(rec, kSyncStage1, true);
-    } else if (stage == 2) {
-        flow_wait(rec, kSyncStage1, kFColTiles, err);
-        row_fwd_tile<kFRowsPerTile>(b, t, p.work, p.xs, p.twh, p.tws, lds);
-        flow_signal(rec, kSyncStage2, false);
-    } else {
-        flow_wait(rec, kSyncStage2, kFRowTiles, err);
-        route_task<LAYOUT, true>(t, b, p.xs, p.cre, p.cim, p.rec, p.tasks, p.ncoef, SliceMap{nullptr, 1, 0},
-                                 p.tws, lds);
-        flow_finish(rec, (unsigned)p.ntasks);
+    __shared__ int sh[4];
+    const int x = (int)(xcc_id() & (kFlowQueues - 1));
+    const long K = flow_slices(p.batch, x);
+    long next = -1;
+    int it = 0;
+    trace_at(p, kTraceTasks - 1, 0, clock100());
+    trace_at(p, kTraceTasks - 1, 1, (unsigned long long)x);
+    for (;;) {
+        long b;
+        int t;
+        trace_at(p, it, 1, clock100());
+        const int stage = flow_next(p, x, K, sh, b, t, next);
+        trace_at(p, it, 2, clock100());
+        if (stage == 0) {
+            trace_at(p, kTraceTasks - 1, 2, clock100());
+            break;
+        }
+        trace_at(p, it, 0, (unsigned long long)stage | ((unsigned long long)b << 8) | ((unsigned long long)t << 40));
+        int tid;
+        const FlowArgs q = flow_task_args(p, tid);
+        if (stage == 1) {
+            col_fwd_tile<false, kFColsPerTile>((int)b, t, q.x, q.work, q.twp, q.tws,
+                                               SliceSrc{nullptr, nullptr, 1, 1, 0, 0, 0, nullptr, 1, 1, 1}, lds, tid);
+        } else if (stage == 2) {
+            row_fwd_tile<kFRowsPerTile>((int)b, t, q.work, q.xs, q.twh, q.tws, lds, tid);
+        } else {
+            route_task<LAYOUT, WT>(t, (int)b, q.xs, q.cre, q.cim, q.rec, q.tasks, q.ncoef, SliceMap{nullptr, 1, 0},
+                                   q.tws, lds, tid);
+        }
+        trace_at(p, it, 3, clock100());
+        flow_done(p, stage, b);
+        trace_at(p, it, 4, clock100());
+        ++it;
     }
+    flow_exit(p, sh);
 }
 
-template <int LAYOUT>
+template <int LAYOUT, bool WT>
 __global__ __launch_bounds__(kFlowThreads) void k_flow_synthesis(const FlowArgs p) {
     __shared__ float2 lds[kFlowLds];
-    int b = 0, t = 0;
-    const int stage = flow_place(p.ntasks, kFInvColTiles, kFRowTiles, p.batch, b, t);
-    if (stage == 0) return;
-    unsigned* rec = p.sync + (long)b * FCQT_SYNC_PER_SLICE;
-    unsigned* err = p.sync + (long)p.batch * FCQT_SYNC_PER_SLICE;
-    if (stage == 1) {
-        scatter_task<LAYOUT, false>(t, b, p.cre, p.cim, p.f, p.rec, p.tasks, p.ncoef,
-                                    SliceMap{nullptr, 1, 0}, p.tws, lds);
-        flow_signal(rec, kSyncStage1, true);
-    } else if (stage == 2) {
-        flow_wait(rec, kSyncStage1, (unsigned)p.ntasks, err);
-        col_inv_tile<kFInvColsPerTile, false>(b, t, reinterpret_cast<const float2*>(p.f), p.work, p.twp, p.twh, p.ovf,
-                                       p.tws, lds);
-        flow_signal(rec, kSyncStage2, false);
-    } else {
-        flow_wait(rec, kSyncStage2, kFInvColTiles, err);
-        row_inv_tile<kFRowsPerTile, false>(b, t, p.work, p.y, p.tws, lds);
-        flow_finish(rec, kFRowTiles);
+    __shared__ int sh[4];
+    const int x = (int)(xcc_id() & (kFlowQueues - 1));
+    const long K = flow_slices(p.batch, x);
+    long next = -1;
+    int it = 0;
+    trace_at(p, kTraceTasks - 1, 0, clock100());
+    trace_at(p, kTraceTasks - 1, 1, (unsigned long long)x);
+    for (;;) {
+        long b;
+        int t;
+        trace_at(p, it, 1, clock100());
+        const int stage = flow_next(p, x, K, sh, b, t, next);
+        trace_at(p, it, 2, clock100());
+        if (stage == 0) {
+            trace_at(p, kTraceTasks - 1, 2, clock100());
+            break;
+        }
+        trace_at(p, it, 0, (unsigned long long)stage | ((unsigned long long)b << 8) | ((unsigned long long)t << 40));
+        int tid;
+        const FlowArgs q = flow_task_args(p, tid);
+        if (stage == 1) {
+            scatter_task<LAYOUT, false>(t, (int)b, q.cre, q.cim, q.f, q.rec, q.tasks, q.ncoef,
+                                        SliceMap{nullptr, 1, 0}, q.tws, lds, tid);
+        } else if (stage == 2) {
+            col_inv_tile<kFInvColsPerTile, false>((int)b, t, reinterpret_cast<const float2*>(q.f), q.work, q.twp,
+                                                  q.twh, q.ovf, q.tws, lds, tid);
+        } else {
+            row_inv_tile<kFRowsPerTile, WT>((int)b, t, q.work, q.y, q.tws, lds, tid);
+        }
+        trace_at(p, it, 3, clock100());
+        flow_done(p, stage, b);
+        trace_at(p, it, 4, clock100());
+        ++it;
     }
+    flow_exit(p, sh);
 }
 
-// Workgroups of a flow grid: eight residues, each with the stages of the
-// largest share of slices.
-static dim3 flow_grid(int64_t batch, int per_slice) {
-    return dim3((unsigned)(kXcds * ((batch + kXcds - 1) / kXcds) * per_slice));
+// Workgroups per queue: enough for the largest queue's tasks, at most the
+// slots of one XCD: 32 CUs x 8 workgroups for the analysis (LDS-bound; its
+// kernel is held to 4 waves per SIMD, 127 VGPRs) and x 6 for the synthesis
+// (its loop needs 147 VGPRs, 3 waves per SIMD; held to 128 it spills).
+constexpr int kFlowSlotsAnalysis = 256, kFlowSlotsSynthesis = 192;
+constexpr int kFlowSlotsPerXcd = kFlowSlotsAnalysis;
+
+static dim3 flow_grid(int64_t batch, const FlowOrder& o, int slots) {
+    const int64_t per = std::min<int64_t>(slots, flow_end(o, flow_slices(batch, 0)));
+    return dim3((unsigned)(kFlowQueues * std::max<int64_t>(per, 1)));
 }
 
-static int check_flow_args(const fcqt_tables* tab, const uint32_t* sync, int64_t batch) {
+static int check_flow_args(const uint32_t* sync, int64_t batch, const FlowOrder& o) {
     if (!sync) return FCQT_EARG;
     if (!aligned(sync, 16)) return FCQT_EALIGN;
-    // grid size: 8 ceil(batch / 8) (32 + ntasks) workgroups
-    if (((batch + kXcds - 1) / kXcds) * kXcds * (32 + (int64_t)tab->ntasks) >= ((int64_t)1 << 31)) return FCQT_EARG;
+    if (!flow_order_ok(o)) return FCQT_EARG;
+    // positions of the largest queue, plus one claim per workgroup past its
+    // end, stay below 2^32 (the claim counters are 32-bit)
+    if (flow_end(o, flow_slices(batch, 0)) + kFlowSlotsPerXcd >= ((int64_t)1 << 32)) return FCQT_EARG;
     return FCQT_OK;
 }
+
+// Settings of fcqt_persist_tune: lags per direction and the wait bound.
+// Defaults: the fastest lags of a sweep at B = 1 / 16 / 64 (B = 64 per
+// call: analysis 65.0 us at (4, 16) against 68.8 at (2, 4) and 64.9-66.0 at
+// (4, 8) to (16, 32); synthesis 60.2 us at (4, 8) against 72.2 at (2, 4),
+// 80.7 at (1, 8) and 61.9 at (8, 16); B = 1 and 16 within 0.5 us for all).
+static FlowOrder g_order_analysis{kFColTiles, kFRowTiles, 0, 4, 16};
+static FlowOrder g_order_synthesis{0, kFInvColTiles, kFRowTiles, 4, 8};
+static int64_t g_wait_ticks = kWaitTicksDefault;
 
 }  // namespace fcqt
 
 using namespace fcqt;
+
+extern "C" int fcqt_persist_trace(void* buf, int64_t bytes) {
+#ifdef FCQT_FLOW_TRACE
+    if (!buf) {
+        g_trace = nullptr;
+        return FCQT_OK;
+    }
+    // room for the largest grid either direction launches
+    const int64_t need = (int64_t)kFlowQueues * kFlowSlotsPerXcd * kTraceTasks * kTraceFields * 8;
+    if (bytes < need || !aligned(buf, 8)) return FCQT_EARG;
+    g_trace = static_cast<unsigned long long*>(buf);
+    return FCQT_OK;
+#else
+    (void)buf;
+    (void)bytes;
+    return FCQT_EARG;   // this build records no trace
+#endif
+}
+
+extern "C" int fcqt_persist_tune(int direction, int d1, int d2, int64_t wait_ticks) {
+    if (direction != 0 && direction != 1) return FCQT_EARG;
+    if (d1 < 0 || d2 < d1 || d2 > 64) return FCQT_EARG;
+    FlowOrder& o = direction == 0 ? g_order_analysis : g_order_synthesis;
+    o.d1 = d1;
+    o.d2 = d2;
+    if (wait_ticks >= 0) g_wait_ticks = wait_ticks;
+    return FCQT_OK;
+}
 
 extern "C" int fcqt_persist_analysis(const fcqt_tables* tab, const int32_t* route, const float* x, float* coef_re,
                                      float* coef_im, int layout, float* xs, float* work, uint32_t* sync,
@@ -229,7 +399,9 @@ extern "C" int fcqt_persist_analysis(const fcqt_tables* tab, const int32_t* rout
     if (!route || !x || !xs || !work) return FCQT_EARG;
     if (int e = check_band_args(tab, route, coef_re, coef_im, layout, batch)) return e;
     if (!tab->tw_pass || !tab->tw_half) return FCQT_EARG;
-    if (int e = check_flow_args(tab, sync, batch)) return e;
+    FlowOrder o = g_order_analysis;
+    o.n3 = tab->ntasks;
+    if (int e = check_flow_args(sync, batch, o)) return e;
     if (!aligned(x, 8) || !aligned(xs, 8) || !aligned(work, 8) || !aligned(tab->tw_pass, 8) ||
         !aligned(tab->tw_half, 8))
         return FCQT_EALIGN;
@@ -248,11 +420,21 @@ extern "C" int fcqt_persist_analysis(const fcqt_tables* tab, const int32_t* rout
     p.ncoef = (long)tab->ncoef;
     p.ntasks = tab->ntasks;
     p.batch = (int)batch;
-    const dim3 grid = flow_grid(batch, kFColTiles + kFRowTiles + tab->ntasks);
-    if (layout == FCQT_PLANAR)
-        hipLaunchKernelGGL(k_flow_analysis<FCQT_PLANAR>, grid, dim3(kFlowThreads), 0, stream, p);
-    else
-        hipLaunchKernelGGL(k_flow_analysis<FCQT_INTERLEAVED>, grid, dim3(kFlowThreads), 0, stream, p);
+    p.order = o;
+    p.wait_ticks = (uint64_t)g_wait_ticks;
+#ifdef FCQT_FLOW_TRACE
+    p.trace = g_trace;
+#endif
+    const dim3 grid = flow_grid(batch, o, kFlowSlotsAnalysis);
+    // coefficient stores through the L2 from 4 slices up, as the band kernels
+    const bool wt = batch >= 4;
+    if (layout == FCQT_PLANAR) {
+        if (wt) hipLaunchKernelGGL((k_flow_analysis<FCQT_PLANAR, true>), grid, dim3(kFlowThreads), 0, stream, p);
+        else hipLaunchKernelGGL((k_flow_analysis<FCQT_PLANAR, false>), grid, dim3(kFlowThreads), 0, stream, p);
+    } else {
+        if (wt) hipLaunchKernelGGL((k_flow_analysis<FCQT_INTERLEAVED, true>), grid, dim3(kFlowThreads), 0, stream, p);
+        else hipLaunchKernelGGL((k_flow_analysis<FCQT_INTERLEAVED, false>), grid, dim3(kFlowThreads), 0, stream, p);
+    }
     return launch_status();
 }
 
@@ -262,7 +444,9 @@ extern "C" int fcqt_persist_synthesis(const fcqt_tables* tab, const int32_t* sca
     if (!scat || !ovf || !f || !work || !y) return FCQT_EARG;
     if (int e = check_band_args(tab, scat, coef_re, coef_im, layout, batch)) return e;
     if (!tab->tw_pass || !tab->tw_half) return FCQT_EARG;
-    if (int e = check_flow_args(tab, sync, batch)) return e;
+    FlowOrder o = g_order_synthesis;
+    o.n1 = tab->ntasks;
+    if (int e = check_flow_args(sync, batch, o)) return e;
     if (!aligned(f, 16) || !aligned(y, 8) || !aligned(work, 8) || !aligned(ovf, 4) || !aligned(tab->tw_pass, 8) ||
         !aligned(tab->tw_half, 8))
         return FCQT_EALIGN;
@@ -282,10 +466,21 @@ extern "C" int fcqt_persist_synthesis(const fcqt_tables* tab, const int32_t* sca
     p.ncoef = (long)tab->ncoef;
     p.ntasks = tab->ntasks;
     p.batch = (int)batch;
-    const dim3 grid = flow_grid(batch, tab->ntasks + kFInvColTiles + kFRowTiles);
-    if (layout == FCQT_PLANAR)
-        hipLaunchKernelGGL(k_flow_synthesis<FCQT_PLANAR>, grid, dim3(kFlowThreads), 0, stream, p);
-    else
-        hipLaunchKernelGGL(k_flow_synthesis<FCQT_INTERLEAVED>, grid, dim3(kFlowThreads), 0, stream, p);
+    p.order = o;
+    p.wait_ticks = (uint64_t)g_wait_ticks;
+#ifdef FCQT_FLOW_TRACE
+    p.trace = g_trace;
+#endif
+    const dim3 grid = flow_grid(batch, o, kFlowSlotsSynthesis);
+    // output stores through the L2 at the batches where the wide inverse
+    // passes use them
+    const bool wt = batch >= 4 && batch <= kInvWriteThroughMaxBatch;
+    if (layout == FCQT_PLANAR) {
+        if (wt) hipLaunchKernelGGL((k_flow_synthesis<FCQT_PLANAR, true>), grid, dim3(kFlowThreads), 0, stream, p);
+        else hipLaunchKernelGGL((k_flow_synthesis<FCQT_PLANAR, false>), grid, dim3(kFlowThreads), 0, stream, p);
+    } else {
+        if (wt) hipLaunchKernelGGL((k_flow_synthesis<FCQT_INTERLEAVED, true>), grid, dim3(kFlowThreads), 0, stream, p);
+        else hipLaunchKernelGGL((k_flow_synthesis<FCQT_INTERLEAVED, false>), grid, dim3(kFlowThreads), 0, stream, p);
+    }
     return launch_status();
 }

@@ -12,8 +12,15 @@ import pathlib
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflashcqt.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 SYNC_PER_SLICE = 64       # FCQT_SYNC_PER_SLICE: uint32 per slice in a single-launch counter buffer
+SYNC_HEAD_WORDS = 320     # FCQT_SYNC_HEAD_WORDS: the error word, exit count and per-XCD queue claims
+
+
+def sync_words(batch):
+    """FCQT_SYNC_WORDS(batch): uint32 words of a single-launch sync buffer;
+    word batch * SYNC_PER_SLICE is the error word."""
+    return batch * SYNC_PER_SLICE + SYNC_HEAD_WORDS
 PLANAR = 0
 INTERLEAVED = 1
 
@@ -25,7 +32,7 @@ EXPORTS = ("fcqt_abi_version", "fcqt_status_string", "fcqt_last_hip_error",
            "fcqt_overlap_add", "fcqt_stream_overlap", "fcqt_image_check", "fcqt_tables_upload",
            "fcqt_workspace_sizes", "fcqt_analysis_static", "fcqt_persist_analysis", "fcqt_persist_synthesis",
            "fcqt_stream_analysis", "fcqt_stream_synthesis", "fcqt_sliced_analysis",
-           "fcqt_sliced_synthesis")
+           "fcqt_sliced_synthesis", "fcqt_persist_tune", "fcqt_persist_trace")
 
 
 class Tables(ctypes.Structure):
@@ -60,7 +67,7 @@ class NativeError(RuntimeError):
 _lib = None
 _variants = {}
 #: variant libraries (same C ABI, other kernel builds): name -> file in _lib/
-VARIANTS = {"xlane": "libflashcqt_xlane.so"}
+VARIANTS = {"xlane": "libflashcqt_xlane.so", "flowtrace": "libflashcqt_flowtrace.so"}
 
 
 def load():
@@ -75,8 +82,9 @@ def load():
 def load_variant(name):
     """Load and type a variant library built beside the library (its C ABI
     is the library's): "xlane" runs the band units of M <= 256 with the
-    cross-lane exchange between their first two stages. Raises NativeError
-    if it is not built."""
+    cross-lane exchange between their first two stages; "flowtrace" records
+    the single-launch kernels' stage trace (fcqt_persist_trace). Raises
+    NativeError if it is not built."""
     if name not in _variants:
         if name not in VARIANTS:
             raise NativeError(f"unknown library variant {name!r}")
@@ -120,6 +128,8 @@ def _open(path):
         "fcqt_analysis_static": ([T, P, P, P, P, ctypes.c_int, I64, S], ctypes.c_int),
         "fcqt_persist_analysis": ([T, P, P, P, P, ctypes.c_int, P, P, P, I64, S], ctypes.c_int),
         "fcqt_persist_synthesis": ([T, P, P, P, P, ctypes.c_int, P, P, P, P, I64, S], ctypes.c_int),
+        "fcqt_persist_tune": ([ctypes.c_int, ctypes.c_int, ctypes.c_int, I64], ctypes.c_int),
+        "fcqt_persist_trace": ([P, I64], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -147,23 +147,37 @@ class FusedOctCQT:
         return w["FA"]
 
     def sync_buffer(self, B):
-        """Stage counters of the single-launch directions for batch B
-        ((B + 1) * FCQT_SYNC_PER_SLICE uint32), zeroed on first use; every
-        call returns them to zero. The last block is the error word."""
+        """Counters of the single-launch directions for batch B
+        (FCQT_SYNC_WORDS(B) uint32: per-slice stage counts, then the error
+        word, the exit count and the per-XCD queue claims), zeroed on first
+        use; a call that succeeds returns every word to zero."""
         w = self._workspace(B)
         if "SYNC" not in w:
             with torch.cuda.device(self.dev):
-                w["SYNC"] = torch.zeros((B + 1) * _native.SYNC_PER_SLICE, dtype=torch.int32, device=self.dev)
+                w["SYNC"] = torch.zeros(_native.sync_words(B), dtype=torch.int32, device=self.dev)
             self._wp[B]["SYNC"] = w["SYNC"].data_ptr()
         return w["SYNC"]
 
     def sync_error(self, B):
-        """The single-launch error word for batch B (0: every stage wait ended
-        in time and on the right XCD). Reads device memory: synchronizes.
-        After a nonzero word the failed call may have left slice counters
-        set: zero the whole buffer (`sync_buffer(B).zero_()`) before the
-        next single-launch call."""
+        """The single-launch error word for batch B: 0 when every call so far
+        completed; bit 1: a stage wait outlasted its bound; bit 4: a queue
+        was served by no workgroup (no workgroup ran on one of the XCDs).
+        Reads device memory: synchronizes."""
         return int(self.sync_buffer(B)[B * _native.SYNC_PER_SLICE].item())
+
+    def sync_reset(self, B):
+        """After a nonzero error word: wait for the device, then zero the
+        whole sync buffer (a failed call leaves its counters as they were)."""
+        torch.cuda.synchronize(self.dev)
+        self.sync_buffer(B).zero_()
+        torch.cuda.synchronize(self.dev)
+
+    def _persist_checked(self, B, what):
+        err = self.sync_error(B)
+        if err:
+            self.sync_reset(B)
+            raise _native.NativeError(f"{what}: single-launch error word {err} (1: a stage wait timed out, "
+                                      f"4: an XCD's queue was not served); the results are not valid")
 
     def _fbuf(self, table, B):
         return self._workspace(B)["F"] if table == "scat" else self.fa_buffer(B)
@@ -391,12 +405,19 @@ class FusedOctCQT:
 
     # --------------------------------------- reference entry points kept
 
-    def persist_fwd(self, x):
+    def persist_fwd(self, x, check=True):
         """The reference's single-launch forward (fused.py:748-762,
         persist2.cu:140-161): the whole analysis as one launch
-        (fcqt_persist_analysis: column tiles, row tiles and band tasks of a
-        slice on one XCD, each stage waiting for the slice's previous one).
-        Same outputs as fwd, bit for bit (workspace views)."""
+        (fcqt_persist_analysis: persistent workgroups take the column tiles,
+        row tiles and band tasks of the slices of their own XCD from a
+        queue, each task waiting for its slice's previous stage). Same
+        outputs as fwd, bit for bit (workspace views).
+
+        check=True reads the call's error word (one device synchronization)
+        and raises NativeError, after zeroing the sync buffer, when it is
+        nonzero. check=False leaves that to the caller (graph capture, or
+        timing without host synchronizations): call sync_error(B) after the
+        calls or replays and sync_reset(B) if it is nonzero."""
         self._check_x(x)
         B = x.shape[0]
         w = self._workspace(B)
@@ -405,15 +426,16 @@ class FusedOctCQT:
         _native.check(self.lib.fcqt_persist_analysis(self._ct, self._tp["route"], x.data_ptr(), p["KR"], p["KI"],
                                                      _native.PLANAR, p["X"], p["W"], p["SYNC"], B,
                                                      _native.stream_handle(self.dev.index)), "persist_analysis")
+        if check:
+            self._persist_checked(B, "persist_analysis")
         return w["KR"], w["KI"]
 
-    def persist_inv(self, KR, KI):
+    def persist_inv(self, KR, KI, check=True):
         """The reference's single-launch inverse (fused.py:764-778,
         persist2.cu:163-222): the whole synthesis as one launch
-        (fcqt_persist_synthesis: band scatter, inverse column tiles and
-        inverse row tiles of a slice on one XCD, each stage waiting for the
-        slice's previous one). Same output as bwd, bit for bit (a workspace
-        view)."""
+        (fcqt_persist_synthesis: band scatter tasks, inverse column tiles
+        and inverse row tiles, as persist_fwd). Same output as bwd, bit for
+        bit (a workspace view). check: as persist_fwd."""
         B = KR.shape[0] if KR.dim() else 0
         if B < 1 or KR.shape != (B, self.ncoef) or KI.shape != (B, self.ncoef):
             raise ValueError(f"KR, KI must be [B, {self.ncoef}]")
@@ -428,6 +450,8 @@ class FusedOctCQT:
                                                       KR.data_ptr(), KI.data_ptr(), _native.PLANAR, p["F"], p["W"],
                                                       p["XO"], p["SYNC"], B, _native.stream_handle(self.dev.index)),
                       "persist_synthesis")
+        if check:
+            self._persist_checked(B, "persist_synthesis")
         return w["XO"]
 
     def bench_parts(self, x, reps=50):

@@ -16,15 +16,19 @@
  *   - Complex buffers are interleaved fp32 pairs (re, im), 8-byte aligned.
  *     Record tables (int32 quadruples) must be 16-byte aligned.
  *   - All work is enqueued asynchronously on `stream` (any HIP stream,
- *     including one under hipGraph capture); no call synchronises, allocates
- *     or issues hipMemset, so every call can be captured into a graph.
+ *     including one under hipGraph capture); no call allocates or issues
+ *     hipMemset, so every call can be captured into a graph. The one call
+ *     that synchronises is the set-up call fcqt_tables_upload.
  *   - Return value: FCQT_OK (0), or an FCQT_E* code. Argument errors are
  *     detected before any HIP call is made.
  *   - Calls that share a workspace must be ordered on one stream.
- *   - Results are deterministic: no kernel uses atomics. They are also
- *     independent of the batch size: a slice gives the same bits alone or
- *     in any batch (the launchers pick the FFT passes' tile shape by batch
- *     size; every shape does the same arithmetic per slice).
+ *   - Results are deterministic: no result is accumulated with atomics
+ *     (every output value has one writer). Atomics appear only as counters
+ *     (the single-launch kernels' queues and stage counts) and as
+ *     write-through stores of final values. Results are also independent of
+ *     the batch size: a slice gives the same bits alone or in any batch
+ *     (the launchers pick the FFT passes' tile shape by batch size; every
+ *     shape does the same arithmetic per slice).
  *
  * Fixed geometry (the reference's fused path hard-requires it,
  * fused.py:230): N = 65536 real samples per slice, L = N/2 = 32768.
@@ -39,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FCQT_ABI_VERSION 12
+#define FCQT_ABI_VERSION 13
 
 #define FCQT_N 65536          /* real samples per slice */
 #define FCQT_L 32768          /* packed complex length */
@@ -135,7 +139,7 @@ typedef struct fcqt_sizes {
     int64_t scatter;     /* f, one per scatter table: batch * FCQT_FROW complex */
     int64_t coef_plane;  /* one FCQT_PLANAR plane: batch * ncoef fp32 (FCQT_INTERLEAVED: twice this) */
     int64_t tail;        /* fcqt_stream_overlap tail: batch (signals) * 32768 fp32 */
-    int64_t sync;        /* single-launch stage counters: (batch + 1) * FCQT_SYNC_PER_SLICE uint32 */
+    int64_t sync;        /* single-launch counters: FCQT_SYNC_WORDS(batch) uint32 */
 } fcqt_sizes;
 
 /* Fill *out for `batch` slices (tab supplies ncoef). FCQT_EARG on a bad
@@ -232,30 +236,66 @@ int fcqt_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
 
 /* Single-launch directions: the same transforms as fcqt_analysis and
  * fcqt_synthesis (same buffers and rules, same results bit for bit), each
- * as ONE ordinary launch. Its three stages (analysis: column tiles, row
- * tiles, band tasks; synthesis: band tasks, inverse column tiles, inverse
- * row tiles) are workgroups of the same grid; a slice's stages all run on
- * one XCD and each waits, through counters in `sync`, for the stage of the
- * same slice before it, so there is no grid-wide barrier.
- *   sync  uint32 [(batch + 1) * FCQT_SYNC_PER_SLICE] (fcqt_sizes.sync
- *         bytes), 16-byte aligned, zero-filled once when allocated
- *         (fcqt_fill_zero); every call leaves the slice counters at zero
- *         again. Word batch * FCQT_SYNC_PER_SLICE is an error word: nonzero
- *         after a call means a stage wait timed out or a stage ran on
- *         another XCD than the stage it waits for, and the results are not
- *         valid; the failed call may also leave slice counters set, so the
- *         caller zero-fills the whole buffer again before the next call.
+ * as ONE ordinary launch of persistent workgroups. A direction has three
+ * stages per slice (analysis: column tiles, row tiles, band tasks;
+ * synthesis: band tasks, inverse column tiles, inverse row tiles). The
+ * slices are split over one queue per XCD (slice b to queue b mod 8), and
+ * the workgroups running on XCD x (as the hardware reports it) take queue
+ * x's tasks one at a time, in an order that interleaves the slices' stages
+ * with lags (fcqt_persist_tune); a stage-2 or stage-3 task waits, through
+ * counters in `sync`, for its slice's previous stage. No grid-wide barrier;
+ * every wait is for a task taken earlier, so every wait ends.
+ *   sync  uint32 [FCQT_SYNC_WORDS(batch)] (fcqt_sizes.sync bytes), 16-byte
+ *         aligned, zero-filled once when allocated (fcqt_fill_zero); a call
+ *         that succeeds leaves every word at zero again. Word
+ *         batch * FCQT_SYNC_PER_SLICE is an error word: nonzero after a call
+ *         means the results are not valid (bit 1: a stage wait outlasted its
+ *         bound, about two seconds; bit 4: a queue that had tasks was served
+ *         by no workgroup, i.e. no workgroup ran on that XCD, as on a chip
+ *         partitioned into fewer XCDs per device). After a nonzero word the
+ *         counters are left as they were: the caller synchronises and
+ *         zero-fills the whole buffer before the next call.
  *         One sync buffer per stream: calls that overlap on one buffer race.
- * Capturable into a hipGraph like every other entry point. Replace the
- * reference's fwd2 / inv2 (persist2.cu:140-222, reached through
- * FusedOctCQT.persist_fwd / persist_inv, fused.py:748-778). */
+ * Capturable into a hipGraph like every other entry point (check the error
+ * word after replay). Replace the reference's fwd2 / inv2
+ * (persist2.cu:140-222, reached through FusedOctCQT.persist_fwd /
+ * persist_inv, fused.py:748-778). */
 #define FCQT_SYNC_PER_SLICE 64
+#define FCQT_SYNC_HEAD_WORDS 320
+#define FCQT_SYNC_WORDS(batch) ((int64_t)(batch) * FCQT_SYNC_PER_SLICE + FCQT_SYNC_HEAD_WORDS)
 int fcqt_persist_analysis(const fcqt_tables* tab, const int32_t* route, const float* x,
                           float* coef_re, float* coef_im, int layout,
                           float* xs, float* work, uint32_t* sync, int64_t batch, hipStream_t stream);
 int fcqt_persist_synthesis(const fcqt_tables* tab, const int32_t* scat, const int32_t* ovf,
                            const float* coef_re, const float* coef_im, int layout,
                            float* f, float* work, float* y, uint32_t* sync, int64_t batch, hipStream_t stream);
+
+/* Process-wide settings of the single-launch kernels, read at each launch
+ * (not for use while another host thread launches them). direction 0: the
+ * analysis, 1: the synthesis. d1 / d2: the lags, in steps of one slice, of
+ * a slice's stage 2 and stage 3 behind its stage 1 in each queue's order
+ * (0 <= d1 <= d2 <= 64); wait_ticks: the bound of every stage wait in
+ * ticks of the 100 MHz clock (default 200000000, two seconds; a negative
+ * value leaves it unchanged). The results do not depend on any of them. No
+ * counterpart in the reference (its persistent kernels use grid-stride
+ * loops with grid-wide barriers). */
+int fcqt_persist_tune(int direction, int d1, int d2, int64_t wait_ticks);
+
+/* Stage trace of the single-launch kernels, in the trace build of the
+ * library only (libflashcqt_flowtrace.so, the same sources built with
+ * FCQT_FLOW_TRACE; the library itself returns FCQT_EARG and records
+ * nothing). Every later single-launch call writes, per workgroup in
+ * blockIdx order, FCQT_TRACE_TASKS records of FCQT_TRACE_FIELDS uint64 into
+ * `buf` (device memory, zero-filled by the caller): record i of the first
+ * FCQT_TRACE_TASKS - 1 is the workgroup's task i, {stage | slice << 8 |
+ * tile << 40, 100 MHz clock before its claim or wait, when ready, body
+ * done, counted in} (a zero first field ends the list); the last record is
+ * {start, XCD, leave}. bytes >= 8 * 256 * FCQT_TRACE_TASKS *
+ * FCQT_TRACE_FIELDS * 8 (the largest grid); buf = NULL stops recording.
+ * No counterpart in the reference. */
+#define FCQT_TRACE_TASKS 32
+#define FCQT_TRACE_FIELDS 6
+int fcqt_persist_trace(void* buf, int64_t bytes);
 
 /* Allocation-free analysis: fcqt_analysis with the spectrum X and the work
  * buffer taken from a static device array of the library (each GPU holds its

@@ -44,9 +44,26 @@ def test_variant_library_exports_the_same_abi():
         _native.load_variant("nope")
 
 
+def test_trace_build_exports_the_same_abi(lib):
+    """The trace build (libflashcqt_flowtrace.so) loads with the library's C
+    ABI; only it accepts a stage-trace buffer (host calls, no GPU): the
+    library refuses one, the trace build refuses one too small and accepts
+    one large enough and a null buffer (recording off)."""
+    from flash_cqt import _native
+    tr = _native.load_variant("flowtrace")
+    for name in declared():
+        assert hasattr(tr, name), name
+    assert tr.fcqt_abi_version() == _native.ABI_VERSION
+    need = 8 * 256 * 32 * 6 * 8
+    assert lib.fcqt_persist_trace(ctypes.c_void_p(4096), need) == 1           # FCQT_EARG: no trace here
+    assert tr.fcqt_persist_trace(ctypes.c_void_p(4096), need - 8) == 1        # too small
+    assert tr.fcqt_persist_trace(ctypes.c_void_p(4096), need) == 0
+    assert tr.fcqt_persist_trace(None, 0) == 0
+
+
 def test_abi_version(lib):
     from flash_cqt import _native
-    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 12
+    assert lib.fcqt_abi_version() == _native.ABI_VERSION == 13
 
 
 def test_header_constants_match_tables_and_kernels():

@@ -24,11 +24,11 @@ def test_header_from_c(tmp_path, factored_tables):
     T.save_image(factored_tables, img)
     r = subprocess.run([str(exe), str(img)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
-    assert "c abi check ok (ABI 12)" in r.stdout
+    assert "c abi check ok (ABI 13)" in r.stdout
     assert f"ncoef {factored_tables['ncoef']}, {factored_tables['tasks'].shape[0]} tasks" in r.stdout
     B = 64
     assert (f"signal {B * T.N * 4} spectrum {B * T.XSTRIDE * 8} work {B * T.L * 8} scatter {B * T.FROW * 8} "
-            f"coef_plane {B * factored_tables['ncoef'] * 4} tail {B * T.N // 2 * 4} sync {(B + 1) * 64 * 4}") in r.stdout
+            f"coef_plane {B * factored_tables['ncoef'] * 4} tail {B * T.N // 2 * 4} sync {(B * 64 + 320) * 4}") in r.stdout
 
 
 @pytest.mark.gpu

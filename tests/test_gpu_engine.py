@@ -864,11 +864,12 @@ def test_reference_entry_points(fused):
 
 @pytest.mark.parametrize("B", [1, 5, 64, 130])
 def test_single_launch_directions_equal_six_launch_bitwise(fused, B):
-    """fcqt_persist_analysis / fcqt_persist_synthesis (one launch per
-    direction, a slice's stages on one XCD waiting on per-slice counters)
-    against the six-launch path, bit for bit. B = 5 leaves three XCDs
-    without a slice; B = 130 has more workgroups than fit at once. After
-    every call the counters are back at zero and the error word is clear."""
+    """fcqt_persist_analysis / fcqt_persist_synthesis (one launch of
+    persistent workgroups per direction, each XCD serving the queue of its
+    slices) against the six-launch path, bit for bit. B = 5 leaves three
+    queues without a slice; B = 130 gives queues of different lengths and
+    more positions than workgroups. After every call every word of the sync
+    buffer is back at zero (counters, claims, error word)."""
     from flash_cqt import _native
     print(f"single-launch directions: batch {B}", flush=True)
     rs = np.random.RandomState(900 + B)
@@ -899,37 +900,102 @@ def test_single_launch_directions_equal_six_launch_bitwise(fused, B):
         assert torch.equal(kc, k) and torch.equal(yi, y) and not sync.any()
 
 
-def test_single_launch_reports_a_foreign_xcd_mark(fused):
-    """The host marks slice 0's record as if other XCDs had run its first
-    stage: the waits still end normally (the counters are untouched), the
-    results are unchanged, and the waiting workgroups report the mismatch
-    in the error word (2). The record itself is cleared by the call. The
-    mark holds two XCD bits, so it differs from the running XCD's single
-    bit whichever hardware XCD id the slice lands on."""
+@pytest.mark.parametrize("B", [1, 64])
+def test_single_launch_directions_match_oracle(fused, oracle, B):
+    """The single-launch directions on their own against the oracle:
+    coefficients >= 120 dB, round trip >= 125 dB on every row (configs[1]'s
+    sinusoids at B = 1, randn at B = 64), and >= 115 dB per band group for
+    the randn batch (the sinusoids leave some groups nearly empty, so their
+    own SNR measures fp32 rounding against almost no signal)."""
+    print(f"single-launch vs oracle: batch {B}", flush=True)
+    if B == 1:
+        x_np = sinusoids()
+    else:
+        x_np = np.random.RandomState(64).standard_normal((B, N)).astype(np.float32)
+    x = gpu(x_np)
+    PR, PI = fused.persist_fwd(x)
+    got = cnp(PR) + 1j * cnp(PI)
+    y = cnp(fused.persist_inv(PR, PI))
+    rows = [0] if B == 1 else [0, 31, B - 1]
+    ref = oracle.flatten(*oracle.fwd(x_np[rows]))
+    db = snr_db(ref, got[rows])
+    rt = min(snr_db(x_np[r], y[r]) for r in range(B))
+    print(f"B={B}: single-launch coefficients {db:.2f} dB, worst-row round trip {rt:.2f} dB")
+    assert db >= 120
+    if B > 1:
+        for b, M, off in fused.gspec:
+            assert snr_db(ref[:, off:off + b * M], got[rows][:, off:off + b * M]) >= 115
+    assert rt >= 125
+
+
+def test_single_launch_order_does_not_change_results(fused):
+    """The lags of the queues' order (fcqt_persist_tune) change when tasks
+    run, never what they compute: several orders, including stage 2 and 3
+    right behind stage 1 (0, 0) and long lags, give the six-launch bits."""
     from flash_cqt import _native
-    B = 1
-    rs = np.random.RandomState(61)
-    x = gpu(rs.standard_normal((B, N)).astype(np.float32))
+    B = 64
+    x = gpu(np.random.RandomState(65).standard_normal((B, N)).astype(np.float32))
+    KR, KI = fused.fwd(x)
+    k = torch.complex(KR, KI).clone()
+    y = fused.bwd(KR, KI).clone()
+    lib = fused.lib
+    try:
+        for d1, d2 in ((0, 0), (1, 1), (0, 6), (8, 8), (3, 17)):
+            print(f"single-launch order lags ({d1}, {d2})", flush=True)
+            _native.check(lib.fcqt_persist_tune(0, d1, d2, -1), "tune")
+            _native.check(lib.fcqt_persist_tune(1, d1, d2, -1), "tune")
+            PR, PI = fused.persist_fwd(x)
+            assert torch.equal(torch.complex(PR, PI), k)
+            assert torch.equal(fused.persist_inv(PR, PI), y)
+        assert lib.fcqt_persist_tune(0, 2, 1, -1) != 0 and lib.fcqt_persist_tune(2, 0, 0, -1) != 0
+    finally:    # the library's defaults
+        _native.check(lib.fcqt_persist_tune(0, 4, 16, -1), "tune")
+        _native.check(lib.fcqt_persist_tune(1, 4, 8, -1), "tune")
+
+
+def test_single_launch_reports_failed_waits(fused):
+    """Failures of the single launch become errors, forced from the host so
+    that every kernel still ends normally: (1) a wait bound of zero ticks
+    (fcqt_persist_tune) makes the first wait that is not met at once give
+    up: the error word gets bit 1, every later wait stops, and persist_fwd
+    raises NativeError after zeroing the sync buffer; (2) an error word left
+    set before a call (as by an unchecked failed call) makes the call give
+    up its waits and raise too. After each, a normal call gives the
+    six-launch bits again."""
+    from flash_cqt import _native
+    B = 64
+    x = gpu(np.random.RandomState(66).standard_normal((B, N)).astype(np.float32))
     KR, KI = fused.fwd(x)
     k = torch.complex(KR, KI).clone()
     sync = fused.sync_buffer(B)
-    sync.zero_()
-    sync[48] = (1 << 5) | (1 << 6)    # slice 0's XCD mark: at least one bit of another XCD
-    PR, PI = fused.persist_fwd(x)
+    lib = fused.lib
+    print("single-launch: wait bound 0", flush=True)
+    _native.check(lib.fcqt_persist_tune(0, 4, 16, 0), "tune")
+    try:
+        with pytest.raises(_native.NativeError, match="error word 1"):
+            fused.persist_fwd(x)
+    finally:
+        _native.check(lib.fcqt_persist_tune(0, 4, 16, 200000000), "tune")
     torch.cuda.synchronize()
+    assert not sync.any()
+    PR, PI = fused.persist_fwd(x)
     assert torch.equal(torch.complex(PR, PI), k)
-    assert fused.sync_error(B) == 2
-    assert not sync[:B * _native.SYNC_PER_SLICE].any()
-    sync.zero_()
-    fused.persist_fwd(x)
+    print("single-launch: error word planted", flush=True)
+    sync[B * _native.SYNC_PER_SLICE] = 1
+    with pytest.raises(_native.NativeError):
+        fused.persist_inv(PR, PI)
+    assert not sync.any()
+    PR, PI = fused.persist_fwd(x)
+    assert torch.equal(torch.complex(PR, PI), k)
     assert fused.sync_error(B) == 0
 
 
 def test_single_launch_directions_replay_in_a_graph(fused):
     """The single-launch directions are ordinary launches: a graph of a
-    round trip through them replays to the eager result every time, with
-    eager work on the same buffers between the replays, and leaves the
-    counters clear."""
+    round trip through them (captured with check=False, the error word read
+    after the replays) replays to the eager result every time, with eager
+    work on the same buffers between the replays, and leaves the sync
+    buffer clear."""
     B = 16
     rs = np.random.RandomState(77)
     x = gpu(rs.standard_normal((B, N)).astype(np.float32))
@@ -939,10 +1005,10 @@ def test_single_launch_directions_replay_in_a_graph(fused):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        fused.persist_inv(*fused.persist_fwd(x))
+        fused.persist_inv(*fused.persist_fwd(x, check=False), check=False)
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=s):
-            fused.persist_inv(*fused.persist_fwd(x))
+            fused.persist_inv(*fused.persist_fwd(x, check=False), check=False)
     torch.cuda.synchronize()
     for _ in range(3):
         fused._workspace(B)["XO"].fill_(float("nan"))

@@ -136,6 +136,6 @@ def test_workspace_sizes(lib, factored_tables):
     assert sz.signal == 64 * T.N * 4 and sz.spectrum == 64 * T.XSTRIDE * 8 and sz.work == 64 * T.L * 8
     assert sz.scatter == 64 * T.FROW * 8 and sz.coef_plane == 64 * factored_tables["ncoef"] * 4
     assert sz.tail == 64 * (T.N // 2) * 4
-    assert sz.sync == 65 * 64 * 4          # (batch + 1) slice records of FCQT_SYNC_PER_SLICE uint32
+    assert sz.sync == (64 * 64 + 320) * 4   # FCQT_SYNC_WORDS(64): slice records, then the head block
     assert lib.fcqt_workspace_sizes(ctypes.byref(tab), 0, ctypes.byref(sz)) == EARG
     assert lib.fcqt_workspace_sizes(None, 1, ctypes.byref(sz)) == EARG
