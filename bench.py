@@ -566,8 +566,7 @@ def peak_memory(cqt_gpu, dev, batches=(1, 8, 16, 32, 64, 128)):
             ours = peak_mb(lambda: f.bwd(*f.fwd(x)))
             lib = peak_mb(lambda: cqt_gpu.bwd(*cqt_gpu.fwd(x)))
         out[str(B)] = {"peak_mb": ours, "peak_mb_per_slice": ours / B, "hipfft_baseline_peak_mb": lib}
-        f._ws.pop(B, None)
-        f._wp.pop(B, None)
+        f.release_workspace()
     table_mb = sum(f.table_bytes.values()) / 1e6
     log("peak MB per round-trip call: " + "  ".join(f"B={b}: {v['peak_mb']:.1f} (hipFFT {v['hipfft_baseline_peak_mb']:.1f})"
                                                     for b, v in out.items()) + f"; tables resident {table_mb:.1f} MB")

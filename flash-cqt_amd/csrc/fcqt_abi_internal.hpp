@@ -16,8 +16,9 @@ constexpr int64_t kMaxBatch = 1 << 22;
 
 // fcqt_analysis runs batches of kAnalysisChunkMinBatch slices and more in
 // chunks of kAnalysisChunk (the measurements are at the loop in abi.hip)
-constexpr int64_t kAnalysisChunk = 128;
-constexpr int64_t kAnalysisChunkMinBatch = 256;
+constexpr int64_t kAnalysisChunk = FCQT_ANALYSIS_CHUNK;
+constexpr int64_t kAnalysisChunkMinBatch = FCQT_ANALYSIS_CHUNK_MIN_BATCH;
+static_assert(kAnalysisChunk == 128 && kAnalysisChunkMinBatch == 256, "chunk constants of the header");
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 

@@ -4,12 +4,12 @@ Same surface as the reference's FusedOctCQT (fused.py:226-243, 787-801,
 918-1080): construct from an OctCQT, then
     KR, KI = f.fwd(x)      # x [B, 65536] fp32 -> coefficient planes [B, ncoef]
     XO     = f.bwd(KR, KI) # -> [B, 65536]
-Outputs are workspace tensors reused across calls of the same batch size (as
-in the reference); clone them to keep results. Graph capture (Graphed or
+Outputs are views of the engine's workspace, reused by the next call (the
+reference reuses them per batch size); clone them to keep results. Graph capture (Graphed or
 torch.cuda.graph, i.e. hipGraph) records the launches as they are.
 
 Pipeline (all launches on the current stream, no host sync, no allocation
-after the first call for a batch size):
+after the first call at the largest batch size so far):
   analysis   column pass -> row pass (untangle: X = rfft(x))
              -> windowed band gathers + band IDFT              (3 kernels)
   synthesis  band DFT + slot scatter -> column pass (slot sum, retangle)
@@ -40,6 +40,15 @@ def _np_groups(cqt):
 
 
 SKEW = 4096      # floats (16 KiB): KR-to-KI plane gap, and offset of F into its allocation
+
+ANALYSIS_CHUNK, ANALYSIS_CHUNK_MIN_BATCH = 128, 256     # FCQT_ANALYSIS_CHUNK, FCQT_ANALYSIS_CHUNK_MIN_BATCH
+
+
+def sliced_analysis_rows(batch):
+    """FCQT_SLICED_ANALYSIS_ROWS: the rows of xs and work a whole-signal
+    sliced analysis of `batch` slices uses (its chunks reuse the leading
+    128 rows from 256 slices on)."""
+    return batch if batch < ANALYSIS_CHUNK_MIN_BATCH else ANALYSIS_CHUNK
 
 
 def slot_buffer(B, dev):
@@ -106,18 +115,39 @@ class FusedOctCQT:
         # the reference exposes its band-engine tables as .radix (fused.py:430);
         # here the same name holds this engine's tables (formats in tables.py)
         self.radix = self.tables
-        self._ws = {}
-        self._wp = {}
+        self._full = None      # the one buffer set (see _workspace)
+        self._recorded = []    # sets a captured graph still uses
+        self._ws = {}          # batch size -> views of the set's leading rows
+        self._wp = {}          # batch size -> their raw pointers
 
     # ------------------------------------------------------------ buffers
 
     def _workspace(self, B):
-        """Per-batch-size buffers of fwd/bwd: X, W, F (the synthesis scatter
+        """The buffers of fwd/bwd for batch B: X, W, F (the synthesis scatter
         buffer, zeroed once: the slots its table never writes must stay
-        zero), the coefficient planes and the output. The analysis adjoint's
-        own scatter buffer FA is added by fa_buffer, only when an adjoint
-        runs, so inference never holds it."""
-        if B not in self._ws:
+        zero), the coefficient planes KR / KI and the output XO, plus FA
+        (fa_buffer) and SYNC (sync_buffer) once those have been asked for.
+
+        There is one buffer set per engine, sized to the largest batch seen
+        so far; a smaller call gets views of its leading rows. Rows are
+        independent and each F buffer is only ever used with its own scatter
+        table, so the slots that table never writes stay zero in every row,
+        and a successful single-launch call leaves its sync words at zero:
+        the leading rows are valid for every smaller batch. Memory is
+        therefore bounded by the largest call (the reference keeps one set
+        per batch size, trainable.py:65-73). The returned views are
+        overwritten by the next call of any batch size.
+
+        A set that served a call under stream capture (hipGraph) stays
+        allocated when a larger one replaces it: the recorded launches hold
+        its addresses and use them on every replay."""
+        full = self._full
+        if full is None or full["B"] < B:
+            if full is not None and full["captured"]:
+                self._recorded.append(full)
+            self._ws.clear()
+            self._wp.clear()
+            self._full = full = None       # release the old set before allocating the new one
             with torch.cuda.device(self.dev):
                 e = lambda *s: torch.empty(*s, dtype=torch.float32, device=self.dev)
                 z = lambda *s: torch.zeros(*s, dtype=torch.float32, device=self.dev)
@@ -130,33 +160,59 @@ class FusedOctCQT:
                 # kernel ran 10-12% slower
                 n = B * self.ncoef
                 planes = z(2 * n + SKEW)
-                self._ws[B] = dict(X=e(B, T.XSTRIDE, 2), W=e(B, L, 2), F=slot_buffer(B, self.dev),
-                                   KR=planes[:n].view(B, self.ncoef),
-                                   KI=planes[n + SKEW:].view(B, self.ncoef), XO=z(B, N))
-            self._wp[B] = {k: v.data_ptr() for k, v in self._ws[B].items()}
+                self._full = full = dict(B=B, captured=False, X=e(B, T.XSTRIDE, 2), W=e(B, L, 2),
+                                         F=slot_buffer(B, self.dev), KR=planes[:n], KI=planes[n + SKEW:],
+                                         XO=z(B, N))
+        if B not in self._ws:
+            nc = B * self.ncoef
+            w = dict(X=full["X"][:B], W=full["W"][:B], F=full["F"][:B],
+                     KR=full["KR"][:nc].view(B, self.ncoef), KI=full["KI"][:nc].view(B, self.ncoef),
+                     XO=full["XO"][:B])
+            if "FA" in full:
+                w["FA"] = full["FA"][:B]
+            if "SYNC" in full:
+                w["SYNC"] = full["SYNC"][:_native.sync_words(B)]
+            self._ws[B] = w
+            self._wp[B] = {k: v.data_ptr() for k, v in w.items()}
+        if torch.cuda.is_current_stream_capturing():
+            full["captured"] = True
         return self._ws[B]
+
+    def release_workspace(self):
+        """Drop the engine's buffer set (a set recorded by a graph capture
+        stays with the graph's engine); the next call allocates afresh."""
+        if self._full is not None and self._full["captured"]:
+            self._recorded.append(self._full)
+        self._full = None
+        self._ws.clear()
+        self._wp.clear()
+
+    def _add_full(self, name, make):
+        """Add a lazily allocated buffer (FA, SYNC) to the current set and to
+        every batch size's views of it."""
+        full = self._full
+        if name not in full:
+            with torch.cuda.device(self.dev):
+                full[name] = make(full["B"])
+            for B, w in self._ws.items():
+                w[name] = full[name][:B] if name != "SYNC" else full[name][:_native.sync_words(B)]
+                self._wp[B][name] = w[name].data_ptr()
 
     def fa_buffer(self, B):
         """The analysis-adjoint scatter buffer for batch B, allocated and
         zeroed on first use (it belongs to the scat_a table only)."""
-        w = self._workspace(B)
-        if "FA" not in w:
-            with torch.cuda.device(self.dev):
-                w["FA"] = slot_buffer(B, self.dev)
-            self._wp[B]["FA"] = w["FA"].data_ptr()
-        return w["FA"]
+        self._workspace(B)
+        self._add_full("FA", lambda n: slot_buffer(n, self.dev))
+        return self._ws[B]["FA"]
 
     def sync_buffer(self, B):
         """Counters of the single-launch directions for batch B
         (FCQT_SYNC_WORDS(B) uint32: per-slice stage counts, then the error
         word, the exit count and the per-XCD queue claims), zeroed on first
         use; a call that succeeds returns every word to zero."""
-        w = self._workspace(B)
-        if "SYNC" not in w:
-            with torch.cuda.device(self.dev):
-                w["SYNC"] = torch.zeros(_native.sync_words(B), dtype=torch.int32, device=self.dev)
-            self._wp[B]["SYNC"] = w["SYNC"].data_ptr()
-        return w["SYNC"]
+        self._workspace(B)
+        self._add_full("SYNC", lambda n: torch.zeros(_native.sync_words(n), dtype=torch.int32, device=self.dev))
+        return self._ws[B]["SYNC"]
 
     def sync_error(self, B):
         """The single-launch error word for batch B: 0 when every call so far
@@ -169,7 +225,8 @@ class FusedOctCQT:
         """After a nonzero error word: wait for the device, then zero the
         whole sync buffer (a failed call leaves its counters as they were)."""
         torch.cuda.synchronize(self.dev)
-        self.sync_buffer(B).zero_()
+        self.sync_buffer(B)
+        self._full["SYNC"].zero_()
         torch.cuda.synchronize(self.dev)
 
     def _persist_checked(self, B, what):
@@ -203,6 +260,16 @@ class FusedOctCQT:
             raise ValueError(f"{name} must be contiguous float32/complex64")
         if t.numel() * t.element_size() != nbytes:
             raise ValueError(f"{name} has {t.numel() * t.element_size()} bytes, expected {nbytes}")
+
+    def _need_rows(self, t, rows, row_bytes, name):
+        """As _need for a buffer of at least `rows` rows of row_bytes (the
+        kernels use its leading rows)."""
+        if not torch.is_tensor(t):
+            raise ValueError(f"{name} must be a tensor")
+        nb = t.numel() * t.element_size()
+        if nb < rows * row_bytes or nb % row_bytes:
+            raise ValueError(f"{name} has {nb} bytes, expected whole rows of {row_bytes} bytes, at least {rows}")
+        self._need(t, nb, name)
 
     def _need_coef(self, re, im, layout, B, name):
         if layout == _native.PLANAR:
@@ -306,15 +373,18 @@ class FusedOctCQT:
     def sliced_analysis(self, sig, window, nslices, coef, xs, work, table="route"):
         """slice_fft then route_bands_sliced of whole signals sig [nsig, len]
         in one call (fcqt_sliced_analysis: from 256 slices on in chunks of
-        about 128 slices, same bits)."""
+        about 128 slices, same bits). xs and work hold at least
+        sliced_analysis_rows(nsig * nslices) rows: every row below 256
+        slices, the 128 rows of one chunk from 256 on."""
         if sig.dim() != 2 or sig.shape[1] < 1:
             raise ValueError("sig must be [nsig, len]")
         nsig, length = sig.shape
         self._need(sig, nsig * length * 4, "sig")
         self._need(window, N * 4, "window")
         B = nsig * nslices
-        self._need(xs, B * T.XSTRIDE * 8, "xs")
-        self._need(work, B * L * 8, "work")
+        rows = sliced_analysis_rows(B)
+        self._need_rows(xs, rows, T.XSTRIDE * 8, "xs")
+        self._need_rows(work, rows, L * 8, "work")
         self._need(coef, B * self.ncoef * 8, "coef")
         _native.check(self.lib.fcqt_sliced_analysis(self._ct, _native.ptr(self.tables[table]),
                                                     _native.ptr(self.tables["slice_groups"]), _native.ptr(sig), length,

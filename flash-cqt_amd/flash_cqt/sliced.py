@@ -222,20 +222,26 @@ class SlicedCQT:
             self.__dict__.update(_cache_owner=f, _fused_ws={}, _stream_ptr_cache={})
         return self.__dict__["_fused_ws"], self.__dict__["_stream_ptr_cache"]
 
-    def _ws(self, f, nsig, S, y=False):
-        """Engine buffers for nsig * S slice rows: X, W, F, and with y=True
-        (the streamed synthesis) a slice buffer Y; the whole-signal
-        synthesis overlap-adds inside its row pass and needs none. There is
-        one buffer set per engine, sized to the largest row count seen so
-        far (Y to the largest streamed row count); a smaller call uses its
+    def _ws(self, f, nsig, S, y=False, x="chunk"):
+        """Engine buffers for nsig * S slice rows: W and F, the spectrum X
+        (x="chunk": the whole-signal analysis, which from 256 slices on runs
+        in chunks of 128 slices through the same leading rows, so X holds
+        sliced_analysis_rows rows; x="full": one row per slice, the streamed
+        analysis; x=False: none), and with y=True (the streamed synthesis) a
+        slice buffer Y; the whole-signal synthesis overlap-adds inside its
+        row pass and needs neither X nor Y. There is one
+        buffer set per engine, sized to the largest row count seen so far
+        (X and Y to the largest that asked for them); a smaller call uses
         leading rows. Rows are independent, and F is only ever used with the
         synthesis scatter table, so the slots that table never writes stay
         zero in every row (F is zeroed when allocated). Memory is therefore
         bounded by the largest call, whatever the signal lengths.
 
-        A set (or a Y) that served a call under stream capture (hipGraph)
-        stays allocated after a larger one replaces it: the recorded launches
-        hold its addresses and write into it on every replay."""
+        A set (or an X or Y) that served a call under stream capture
+        (hipGraph) stays allocated after a larger one replaces it: the
+        recorded launches hold its addresses and write into it on every
+        replay."""
+        from .fused import sliced_analysis_rows
         cache, ptrs = self._caches(f)
         B = nsig * S
         full = cache.get("rows")
@@ -246,9 +252,15 @@ class SlicedCQT:
             if full is not None and full["captured"]:
                 cache.setdefault("recorded", []).append(full)
             ptrs.clear()                 # cached raw pointers refer to the old buffers
-            cache["rows"] = full = dict(B=B, captured=False, X=torch.empty(B, T.XSTRIDE, 2, device=dev),
-                                        W=torch.empty(B, T.L, 2, device=dev),
+            cache["rows"] = full = dict(B=B, captured=False, W=torch.empty(B, T.L, 2, device=dev),
                                         F=slot_buffer(B, dev))
+        xr = B if x == "full" else sliced_analysis_rows(B)
+        if x and ("X" not in full or full["X"].shape[0] < xr):
+            from . import tables as T
+            if "X" in full and full["captured"]:
+                cache.setdefault("recorded", []).append({"X": full["X"]})
+            ptrs.clear()
+            full["X"] = torch.empty(xr, T.XSTRIDE, 2, device=f.dev)
         if y and ("Y" not in full or full["Y"].shape[0] < B):
             if "Y" in full and full["captured"]:
                 cache.setdefault("recorded", []).append({"Y": full["Y"]})
@@ -256,7 +268,12 @@ class SlicedCQT:
             full["Y"] = torch.empty(B, self.sl_len, device=f.dev)
         if torch.cuda.is_current_stream_capturing():
             full["captured"] = True
-        return {k: full[k][:B] for k in (("X", "W", "F", "Y") if y else ("X", "W", "F"))}
+        out = {"W": full["W"][:B], "F": full["F"][:B]}
+        if x:
+            out["X"] = full["X"][:xr]
+        if y:
+            out["Y"] = full["Y"][:B]
+        return out
 
     def _tw32(self):
         tw = self.__dict__.get("_tw32_cache")
@@ -309,10 +326,10 @@ class SlicedCQT:
         if nsig * S >= FUSED_OLA_MIN_SLICES:
             # scatter, inverse passes and the overlap-add (in the row pass's
             # store) in one call; no slice buffer
-            ws = self._ws(f, nsig, S)
+            ws = self._ws(f, nsig, S, x=False)
             f.sliced_synthesis(coef, ws["F"], ws["W"], out, nsig, S, n)
         else:
-            ws = self._ws(f, nsig, S, y=True)
+            ws = self._ws(f, nsig, S, y=True, x=False)
             f.scatter_bands_sliced(coef, ws["F"], nsig, S)
             f.packed_ifft(ws["F"], ws["Y"], ws["W"])
             f.overlap_add(ws["Y"], out, nsig, S, n)
@@ -370,7 +387,7 @@ class SlicedCQT:
         bufs, cache = self._caches(f)
         st = cache.get(nsig)
         if st is None:
-            st = {k: v.data_ptr() for k, v in self._ws(f, nsig, 1, y=True).items()}
+            st = {k: v.data_ptr() for k, v in self._ws(f, nsig, 1, y=True, x="full").items()}
             st["tw"] = self._tw32().data_ptr()
             cache[nsig] = st
         elif torch.cuda.is_current_stream_capturing():
@@ -425,8 +442,11 @@ class SlicedCQT:
         k = 0
 
         def one(prev, chunk, k):
+            # the fused step reads hop samples of every row of both pieces:
+            # only when the carried piece has the chunk's own [B, C, hop]
+            # shape (a short or differently shaped piece takes the host path)
             f = self._fused(prev, chunk)
-            if f is not None and chunk.shape[-1] == self.hop:
+            if f is not None and chunk.dim() == 3 and chunk.shape[-1] == self.hop and prev.shape == chunk.shape:
                 return self._stream_slice_fused(f, prev, chunk, k)
             return self._stream_slice_host(prev, chunk, k)
 
@@ -451,6 +471,9 @@ class SlicedCQT:
                 nsig = B * C
                 if tail is None:
                     tail = torch.zeros(B, C, self.hop, dtype=torch.float32, device=f.dev)
+                elif tail.shape != (B, C, self.hop):
+                    raise ValueError(f"stream_bwd: slice {k} has {B} x {C} signals, the stream started with "
+                                     f"{tail.shape[0]} x {tail.shape[1]}")
                 elif not (tail.is_contiguous() and tail.dtype == torch.float32 and tail.device == f.dev):
                     tail = tail.to(device=f.dev, dtype=torch.float32).contiguous()
                 coef = self._block_buffer(f, blocks, side, nsig, 1)

@@ -363,9 +363,16 @@ int fcqt_route_bands_sliced(const fcqt_tables* tab, const int32_t* route, const 
  * and work then serve one chunk at a time, in their leading 128 rows).
  *   sig    [nsig][sig_len] fp32,  window [65536] fp32
  *   coef   nsig * nslices * ncoef complex (interleaved)
- *   xs, work as for fcqt_packed_fft_fwd with batch nsig * nslices
+ *   xs, work as for fcqt_packed_fft_fwd with batch nsig * nslices below 256
+ *          slices, and with batch 128 (FCQT_ANALYSIS_CHUNK) from 256 on:
+ *          only the leading FCQT_SLICED_ANALYSIS_ROWS(nsig * nslices) rows
+ *          are used, so buffers of that many rows suffice
  * Replaces SlicedCQT.fwd's _slice, fwd_bands, _arrange and block permute
  * (sliced.py:106-146) for a whole signal. */
+#define FCQT_ANALYSIS_CHUNK 128
+#define FCQT_ANALYSIS_CHUNK_MIN_BATCH 256
+#define FCQT_SLICED_ANALYSIS_ROWS(batch) \
+    ((batch) < FCQT_ANALYSIS_CHUNK_MIN_BATCH ? (int64_t)(batch) : (int64_t)FCQT_ANALYSIS_CHUNK)
 int fcqt_sliced_analysis(const fcqt_tables* tab, const int32_t* route, const int32_t* groups,
                          const float* sig, int64_t sig_len, const float* window, int64_t nsig,
                          int64_t nslices, float* coef, float* xs, float* work, hipStream_t stream);

@@ -1021,6 +1021,81 @@ def test_single_launch_directions_replay_in_a_graph(fused):
     assert fused.sync_error(B) == 0 and not fused.sync_buffer(B).any()
 
 
+# ---------------------------------------------------- bounded workspace
+
+def test_workspace_bounded_by_the_largest_batch(cqt_gpu):
+    """FusedOctCQT keeps one buffer set, sized to the largest batch seen:
+    after a batch-64 round trip (and a single-launch one, which adds the
+    sync buffer), ten other batch sizes allocate nothing that outlives their
+    call, and every row they return equals the same row of the batch-64 call
+    bit for bit (leading rows of the one set, F's zero slots intact)."""
+    import gc
+    from flash_cqt.fused import FusedOctCQT
+    f = FusedOctCQT(cqt_gpu, _dev())
+    x64 = gpu(np.random.RandomState(70).standard_normal((64, N)).astype(np.float32))
+    xs = {B: x64[:B].clone() for B in (17, 3, 1, 40, 8, 12, 5, 33, 2, 63)}
+    with torch.no_grad():
+        KR, KI = f.fwd(x64)
+        k64 = torch.complex(KR, KI).clone()
+        y64 = f.bwd(KR, KI).clone()
+        f.persist_inv(*f.persist_fwd(x64))
+    del KR, KI
+    gc.collect()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    sets = id(f._full)
+    for B, x in xs.items():
+        print(f"bounded workspace: batch {B}", flush=True)
+        with torch.no_grad():
+            KR, KI = f.fwd(x)
+            assert torch.equal(torch.complex(KR, KI), k64[:B])
+            assert torch.equal(f.bwd(KR, KI), y64[:B])
+            PR, PI = f.persist_fwd(x)
+            assert torch.equal(f.persist_inv(PR, PI), y64[:B])
+        del KR, KI, PR, PI
+        gc.collect()
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_allocated() == base, B
+    assert id(f._full) == sets and f._full["B"] == 64 and not f._recorded
+
+
+def test_sliced_autograd_workspace_bounded(cqt_gpu):
+    """SlicedCQT under autograd (host framing around the differentiable
+    engine, which asks the engine for batch = signals x slices): five signal
+    lengths, longest first, leave the engine's memory where the longest put
+    it: the engine's buffer set keeps its size and no second set appears,
+    and the process's allocated bytes (less the host framing's index maps, a
+    separate cache of at most eight signal lengths) grow by no more than a
+    one-off 2 MiB of torch's own; each step's gradient is finite and
+    nonzero."""
+    import gc
+    from flash_cqt import SlicedCQT
+    s = SlicedCQT(device=_dev())
+    f = s.cqt.f
+    rs = np.random.RandomState(71)
+    lengths = (441000, 100000, 300000, 65536, 200000)
+    base = None
+    for n in lengths:
+        print(f"sliced autograd workspace: length {n}", flush=True)
+        x = gpu(rs.standard_normal((1, 2, n)).astype(np.float32)).requires_grad_(True)
+        bl, sd = s.fwd(x)
+        y = s.bwd(bl, sd, length=n)
+        (y * y).sum().backward()
+        g = x.grad
+        assert torch.isfinite(g).all() and g.abs().sum() > 0
+        del x, bl, sd, y, g
+        gc.collect()
+        torch.cuda.synchronize()
+        maps = sum(t.numel() * t.element_size() for m in s.__dict__.get("_frame_cache", {}).values() for t in m
+                   if torch.is_tensor(t) and t.is_cuda)
+        engine = sum(v.untyped_storage().nbytes() for v in f._full.values() if torch.is_tensor(v))
+        if base is None:
+            base = torch.cuda.memory_allocated() - maps
+            top, engine0 = f._full["B"], engine
+        assert f._full["B"] == top and engine == engine0 and not f._recorded, n
+        assert torch.cuda.memory_allocated() - maps <= base + (2 << 20), n
+
+
 # ------------------------------------------------------------- errors
 
 def test_bad_inputs_rejected(fused):

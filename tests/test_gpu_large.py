@@ -46,8 +46,7 @@ def test_batch_past_32bit_offsets():
         yr = y[list(rows)].clone()
         xr = x[list(rows)].clone()
         del KR, KI, y, x
-        f._ws.clear()
-        f._wp.clear()
+        f.release_workspace()
         gc.collect()
         torch.cuda.empty_cache()
         for j, r in enumerate(rows):
@@ -58,8 +57,7 @@ def test_batch_past_32bit_offsets():
             assert db >= 125, (r, db)
         torch.cuda.synchronize()
     finally:
-        f._ws.clear()
-        f._wp.clear()
+        f.release_workspace()
         del f
         gc.collect()
         torch.cuda.empty_cache()

@@ -302,7 +302,8 @@ def test_sliced_buffer_sets_kept_for_recorded_graphs_cpu(monkeypatch):
     """SlicedCQT's engine buffers: one set, grown to the largest call, smaller
     calls get leading rows. A set that served a call under stream capture is
     kept allocated when a larger set replaces it (recorded launches hold its
-    addresses); an unrecorded set is dropped."""
+    addresses); an unrecorded set is dropped. X is sized to the chunked
+    analysis's rows and only allocated when an analysis asks for it."""
     import types
     from flash_cqt import tables as T
     from flash_cqt.sliced import SlicedCQT
@@ -313,6 +314,7 @@ def test_sliced_buffer_sets_kept_for_recorded_graphs_cpu(monkeypatch):
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: capturing[0])
     w = s._ws(f, 1, 2)
     assert w["X"].shape == (2, T.XSTRIDE, 2) and w["F"].shape == (2, T.FROW, 2) and not w["F"].any()
+    assert "X" not in s._ws(f, 1, 2, x=False)                          # the synthesis needs no X
     first = s._fused_ws["rows"]
     s._ws(f, 1, 3)                                       # grows; the first set was never recorded
     assert s._fused_ws["rows"] is not first and "recorded" not in s._fused_ws
@@ -331,6 +333,18 @@ def test_sliced_buffer_sets_kept_for_recorded_graphs_cpu(monkeypatch):
     capturing[0] = False
     s._ws(f, 4, 1, y=True)                               # a larger Y: the recorded one is kept
     assert s._fused_ws["recorded"][-1]["Y"] is y3 and s._fused_ws["rows"]["Y"].shape == (4, T.N)
+    # from 256 slices on the chunked analysis uses 128 rows of X; W and F
+    # keep every row (the synthesis runs the whole batch); a synthesis-only
+    # engine allocates no X at all
+    big = s._ws(f, 2, 150)
+    assert big["X"].shape[0] == 128 and big["W"].shape[0] == 300 and big["F"].shape[0] == 300
+    assert s._ws(f, 1, 200)["X"].shape[0] == 200 and s._ws(f, 1, 100)["X"].shape[0] == 100   # below 256: no chunks
+    assert s._ws(f, 280, 1, x="full")["X"].shape[0] == 280         # the streamed analysis: one row per slice
+    assert s._ws(f, 1, 300)["X"].shape[0] == 128
+    s2 = SlicedCQT.__new__(SlicedCQT)
+    s2.sl_len = T.N
+    s2._ws(f, 2, 150, x=False)
+    assert "X" not in s2._fused_ws["rows"]
     # the streamed path marks the set it hands out cached pointers for
     s._stream_ptrs = SlicedCQT._stream_ptrs.__get__(s)
     s._tw32 = lambda: torch.zeros(1)
@@ -514,3 +528,29 @@ def test_band_orders_match_the_kernels_and_keep_slices_on_one_xcd_cpu(tmp_path):
             pass_xcd.setdefault(lin & 7, set()).add(ks.xcd_remap(lin, 8 * B) // 8)
         for x in range(8):
             assert per_xcd[x] == pass_xcd[x] == set(range(x * B // 8, (x + 1) * B // 8))
+
+
+def test_stream_fwd_fused_step_needs_matching_pieces_cpu(monkeypatch):
+    """SlicedCQT.stream_fwd takes the fused step (which reads hop samples of
+    every row of both the carried piece and the new chunk) only when both
+    are [B, C, hop] with the same shape; a short piece, or a carried piece of
+    another shape, goes to the host path. Host logic only: the engine and
+    both step bodies are stand-ins that record which path ran."""
+    import types
+    from flash_cqt.sliced import SlicedCQT
+    s = SlicedCQT.__new__(SlicedCQT)
+    s.hop = 8
+    taken = []
+    monkeypatch.setattr(s, "_fused", lambda *t: types.SimpleNamespace(dev=torch.device("cpu")), raising=False)
+    monkeypatch.setattr(s, "_stream_slice_fused", lambda f, prev, chunk, k: taken.append(("fused", k)),
+                        raising=False)
+    monkeypatch.setattr(s, "_stream_slice_host", lambda prev, chunk, k: taken.append(("host", k)), raising=False)
+    full = torch.zeros(2, 1, 8)
+    list(s.stream_fwd([full, full]))
+    assert taken == [("fused", 0), ("fused", 1), ("fused", 2)]
+    taken.clear()
+    list(s.stream_fwd([full, torch.zeros(2, 1, 5), full]))     # a short piece, then a full chunk after it
+    assert taken == [("fused", 0), ("host", 1), ("host", 2), ("fused", 3)]
+    taken.clear()
+    list(s.stream_fwd([torch.zeros(3, 1, 8), full]))           # the carried piece has other signals
+    assert taken == [("fused", 0), ("host", 1), ("fused", 2)]
