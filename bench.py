@@ -265,7 +265,7 @@ def sliced_long(dev):
                "roundtrip_snr_db": snr_db(x, y)}
         res["fwd_ms"] = per_step_ms(lambda: s.fwd(x), steps=10, warm=2)
         res["bwd_ms"] = per_step_ms(lambda: s.bwd(bl, sd, length=L), steps=10, warm=2)
-        ws = s._ws(f, 1, S)
+        ws = s._ws(f, 1, S, x="full")      # the unchunked framing pass needs a row of X per slice
         coef = torch.empty(S * f.ncoef, dtype=torch.complex64, device=dev)
         sig = x.reshape(1, L)
 
