@@ -1021,6 +1021,62 @@ def test_single_launch_directions_replay_in_a_graph(fused):
     assert fused.sync_error(B) == 0 and not fused.sync_buffer(B).any()
 
 
+@pytest.mark.parametrize("B", [8, 64])
+def test_single_launch_trace_shows_the_order_was_kept(cqt_gpu, B):
+    """The trace build of the library (libflashcqt_flowtrace.so) stamps each
+    task of a single-launch call with the chip's clock: every (stage, slice,
+    tile) runs exactly once, on the XCD of its slice's queue, and no stage-2
+    or stage-3 task becomes ready before every task of its slice's previous
+    stage has counted in; the results equal the library's bit for bit."""
+    from flash_cqt import _native
+    from flash_cqt.fused import FusedOctCQT
+    f = FusedOctCQT(cqt_gpu, _dev())
+    ft = FusedOctCQT(cqt_gpu, _dev())
+    ft.lib = _native.load_variant("flowtrace")
+    nt, nf = 32, 6
+    tr = torch.zeros(8 * 256 * nt * nf, dtype=torch.int64, device=_dev())
+    _native.check(ft.lib.fcqt_persist_trace(tr.data_ptr(), tr.numel() * 8), "persist_trace")
+    try:
+        x = gpu(np.random.RandomState(72 + B).standard_normal((B, N)).astype(np.float32))
+        KR, KI = f.fwd(x)
+        k = torch.complex(KR, KI).clone()
+        y = f.bwd(KR, KI).clone()
+        for name in ("analysis", "synthesis"):
+            print(f"single-launch trace: batch {B} {name}", flush=True)
+            tr.zero_()
+            torch.cuda.synchronize()
+            if name == "analysis":
+                PR, PI = ft.persist_fwd(x)
+                assert torch.equal(torch.complex(PR, PI), k)
+                n = (16, 16, ft._ct.ntasks)
+            else:
+                assert torch.equal(ft.persist_inv(KR, KI), y)
+                n = (ft._ct.ntasks, 16, 16)
+            a = tr.view(-1, nt, nf).cpu().numpy().astype(np.int64)
+            seen = {}
+            for w in range(a.shape[0]):
+                if a[w, nt - 1, 0] == 0:
+                    continue
+                xcd = int(a[w, nt - 1, 1])
+                for i in range(nt - 1):
+                    info = int(a[w, i, 0])
+                    if info == 0:
+                        break
+                    key = (info & 0xff, (info >> 8) & 0xffffffff, info >> 40)
+                    assert key not in seen, key
+                    assert key[1] % 8 == xcd, (key, xcd)       # served by its queue's XCD
+                    assert a[w, i, 1] <= a[w, i, 2] <= a[w, i, 3] <= a[w, i, 4]
+                    seen[key] = (a[w, i, 2], a[w, i, 4])       # ready, counted in
+            assert len(seen) == B * sum(n)
+            for (st, b, t), (ready, _) in seen.items():
+                assert 0 <= b < B and 0 <= t < n[st - 1]
+                if st > 1:
+                    last_in = max(seen[(st - 1, b, u)][1] for u in range(n[st - 2]))
+                    assert ready >= last_in, (st, b, t)
+    finally:
+        _native.check(ft.lib.fcqt_persist_trace(None, 0), "persist_trace")
+
+
 # ---------------------------------------------------- bounded workspace
 
 def test_workspace_bounded_by_the_largest_batch(cqt_gpu):
