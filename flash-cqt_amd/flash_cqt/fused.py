@@ -14,7 +14,8 @@ after the first call at the largest batch size so far):
              -> windowed band gathers + band IDFT              (3 kernels)
   synthesis  band DFT + slot scatter -> column pass (slot sum, retangle)
              -> row pass (unpack)                              (3 kernels)
-No kernel uses atomics: every result is bitwise reproducible.
+No result is accumulated with atomics (every output value has one writer):
+every result is bitwise reproducible.
 Table semantics follow fused.py:303-476; see flash_cqt/tables.py.
 """
 import numpy as np
@@ -437,9 +438,9 @@ class FusedOctCQT:
     # ------------------------------------------------- reference surface
 
     # fwd/bwd check only the caller's tensors: the workspace buffers and
-    # tables are the engine's own, sized at allocation, so their pointers are
-    # cached per batch size and passed as they are (host cost per call is
-    # then about that of the kernel launches themselves).
+    # tables are the engine's own, sized at allocation, so the pointers of
+    # each batch size's views are cached and passed as they are (host cost
+    # per call is then about that of the kernel launches themselves).
 
     def fwd(self, x):
         """x [B, 65536] fp32 -> (KR, KI) [B, ncoef], workspace views."""

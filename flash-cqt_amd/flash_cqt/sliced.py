@@ -423,9 +423,40 @@ class SlicedCQT:
         _native.check(f.lib.fcqt_stream_analysis(f._ct, f._tp["route"], f._tp["slice_groups"], pv.data_ptr(), ps,
                                                  cv.data_ptr(), cs, st["tw"], nsig, k, coef.data_ptr(), st["X"],
                                                  st["W"], _native.stream_handle(f.dev.index)), "stream_analysis")
+        views = [coef.as_strided(*a) for a in self._stream_view_args(f, B, C)]
+        # stream_bwd recognises these exact views (by identity, while they are
+        # alive) and reads their buffer in place without re-checking them
+        views[0]._fcqt_stream = (id(f), tuple(id(v) for v in views))
         ng = len(self.oct_bins)
-        views = [coef.as_strided((B, C, b, M), (C * b * M, b * M, M, 1), nsig * off) for b, M, off in f.gspec]
         return views[:ng], views[ng:]
+
+    def _stream_view_args(self, f, B, C):
+        """as_strided arguments of one streamed slice's group views
+        [B, C, bins, M] into its coefficient buffer (cached per B, C)."""
+        cache = self.__dict__.setdefault("_stream_view_cache", {})
+        key = (id(f), B, C)
+        args = cache.get(key)
+        if args is None:
+            nsig = B * C
+            args = cache[key] = [((B, C, b, M), (C * b * M, b * M, M, 1), nsig * off) for b, M, off in f.gspec]
+        return args
+
+    def _stream_buffer(self, blocks, side):
+        """(engine, coefficient buffer) when blocks + side are exactly the
+        views the fused stream_fwd returned for one slice (same objects, no
+        gradient to record), else None."""
+        rec = getattr(blocks[0], "_fcqt_stream", None)
+        if rec is None or side is None:
+            return None
+        f = getattr(self.cqt, "f", None)
+        if f is None or rec[0] != id(f) or not self.fused_framing:
+            return None
+        parts = tuple(blocks) + tuple(side)
+        if len(parts) != len(rec[1]) or any(id(p) != i for p, i in zip(parts, rec[1])):
+            return None
+        if torch.is_grad_enabled() and blocks[0].requires_grad:
+            return None
+        return f, blocks[0]._base
 
     def _stream_slice_host(self, prev, chunk, k):
         hop = chunk.shape[-1]
@@ -465,7 +496,8 @@ class SlicedCQT:
         tail = None
         k = 0
         for blocks, side in slice_coeffs:
-            f = self._fused(*blocks, *(side if side is not None else []))
+            own = self._stream_buffer(blocks, side)
+            f = own[0] if own is not None else self._fused(*blocks, *(side if side is not None else []))
             B, C = blocks[0].shape[:2]
             if f is not None:
                 nsig = B * C
@@ -476,7 +508,7 @@ class SlicedCQT:
                                      f"{tail.shape[0]} x {tail.shape[1]}")
                 elif not (tail.is_contiguous() and tail.dtype == torch.float32 and tail.device == f.dev):
                     tail = tail.to(device=f.dev, dtype=torch.float32).contiguous()
-                coef = self._block_buffer(f, blocks, side, nsig, 1)
+                coef = own[1] if own is not None else self._block_buffer(f, blocks, side, nsig, 1)
                 st = self._stream_ptrs(f, nsig)
                 out = torch.empty(B, C, self.hop, dtype=torch.float32, device=f.dev) if k > 0 else None
                 # scatter, inverse passes and the half-slice overlap-add in one call
