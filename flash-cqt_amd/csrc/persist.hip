@@ -346,9 +346,11 @@ static int check_flow_args(const uint32_t* sync, int64_t batch, const FlowOrder&
     if (!sync) return FCQT_EARG;
     if (!aligned(sync, 16)) return FCQT_EALIGN;
     if (!flow_order_ok(o)) return FCQT_EARG;
-    // positions of the largest queue, plus one claim per workgroup past its
-    // end, stay below 2^32 (the claim counters are 32-bit)
-    if (flow_end(o, flow_slices(batch, 0)) + kFlowSlotsPerXcd >= ((int64_t)1 << 32)) return FCQT_EARG;
+    // positions of the largest queue, plus one claim past its end by every
+    // workgroup of the grid (whatever XCD each lands on), stay below 2^32
+    // (the claim counters are 32-bit)
+    if (flow_end(o, flow_slices(batch, 0)) + (int64_t)kFlowQueues * kFlowSlotsPerXcd >= ((int64_t)1 << 32))
+        return FCQT_EARG;
     return FCQT_OK;
 }
 
