@@ -1121,9 +1121,10 @@ def test_sliced_autograd_workspace_bounded(cqt_gpu):
     lengths, longest first, leave the engine's memory where the longest put
     it: the engine's buffer set keeps its size and no second set appears,
     and the process's allocated bytes (less the host framing's index maps, a
-    separate cache of at most eight signal lengths) grow by no more than a
-    one-off 2 MiB of torch's own; each step's gradient is finite and
-    nonzero."""
+    separate cache of at most eight signal lengths) grow by less than one
+    more buffer set would add (the smallest, for 2 x 3 slices, is 14.6 MB;
+    torch's own one-off allocations have measured 2.0-2.2 MiB, so the bar
+    is 8 MiB); each step's gradient is finite and nonzero."""
     import gc
     from flash_cqt import SlicedCQT
     s = SlicedCQT(device=_dev())
@@ -1149,7 +1150,7 @@ def test_sliced_autograd_workspace_bounded(cqt_gpu):
             base = torch.cuda.memory_allocated() - maps
             top, engine0 = f._full["B"], engine
         assert f._full["B"] == top and engine == engine0 and not f._recorded, n
-        assert torch.cuda.memory_allocated() - maps <= base + (2 << 20), n
+        assert torch.cuda.memory_allocated() - maps <= base + (8 << 20), n
 
 
 # ------------------------------------------------------------- errors
