@@ -319,9 +319,9 @@ def cpu_baseline(batch=64, budget_s=10.0, budget_b1_s=4.0, max_reps=400):
     on a bounded sample of the bench's own workload (batch-`batch` round trips
     of the randn input, about budget_s of CPU work), plus batch 1 on the
     configs[1] input and batches 4 and 16 on randn input (short samples).
-    torch runs with os.cpu_count() threads, as the survey's measurement
-    specifies; the CPUs this process may run on (affinity) and the cgroup CPU
-    quota are reported beside it. The previous thread count is restored."""
+    torch runs with os.cpu_count() threads (every core the host reports); the
+    CPUs this process may run on (affinity) and the cgroup CPU quota are
+    reported beside it. The previous thread count is restored."""
     from oracle.torch_port import TorchPortOctCQT
     cores = os.cpu_count() or 1
     prev_threads = torch.get_num_threads()
