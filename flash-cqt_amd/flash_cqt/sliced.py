@@ -27,6 +27,7 @@ them back to bwd reads that buffer without a copy. The bounded-state stream
 fcqt_stream_synthesis scatters, inverts and overlap-adds).
 """
 import math
+import weakref
 
 import torch
 
@@ -423,12 +424,18 @@ class SlicedCQT:
         _native.check(f.lib.fcqt_stream_analysis(f._ct, f._tp["route"], f._tp["slice_groups"], pv.data_ptr(), ps,
                                                  cv.data_ptr(), cs, st["tw"], nsig, k, coef.data_ptr(), st["X"],
                                                  st["W"], _native.stream_handle(f.dev.index)), "stream_analysis")
-        views = [coef.as_strided(*a) for a in self._stream_view_args(f, B, C)]
-        # stream_bwd recognises these exact views (by identity, while they are
-        # alive) and reads their buffer in place without re-checking them
-        views[0]._fcqt_stream = (id(f), tuple(id(v) for v in views))
+        views = self._stream_mark(f, [coef.as_strided(*a) for a in self._stream_view_args(f, B, C)])
         ng = len(self.oct_bins)
         return views[:ng], views[ng:]
+
+    @staticmethod
+    def _stream_mark(f, views):
+        """Mark one streamed slice's views so that stream_bwd recognises
+        these exact objects (weak references to the engine and to every view:
+        a freed object's address reused by another never matches) and reads
+        their buffer in place without re-checking them."""
+        views[0]._fcqt_stream = (weakref.ref(f), tuple(weakref.ref(v) for v in views))
+        return views
 
     def _stream_view_args(self, f, B, C):
         """as_strided arguments of one streamed slice's group views
@@ -449,10 +456,10 @@ class SlicedCQT:
         if rec is None or side is None:
             return None
         f = getattr(self.cqt, "f", None)
-        if f is None or rec[0] != id(f) or not self.fused_framing:
+        if f is None or rec[0]() is not f or not self.fused_framing:
             return None
         parts = tuple(blocks) + tuple(side)
-        if len(parts) != len(rec[1]) or any(id(p) != i for p, i in zip(parts, rec[1])):
+        if len(parts) != len(rec[1]) or any(r() is not p for p, r in zip(parts, rec[1])):
             return None
         if torch.is_grad_enabled() and blocks[0].requires_grad:
             return None

@@ -554,3 +554,47 @@ def test_stream_fwd_fused_step_needs_matching_pieces_cpu(monkeypatch):
     taken.clear()
     list(s.stream_fwd([torch.zeros(3, 1, 8), full]))           # the carried piece has other signals
     assert taken == [("fused", 0), ("host", 1), ("fused", 2)]
+
+
+def test_stream_bwd_recognises_only_the_marked_views_cpu():
+    """stream_bwd reads a streamed slice's coefficient buffer in place only
+    when it is handed the very view objects stream_fwd marked, from the
+    engine the object uses now: a replaced part, a part of another slice,
+    another engine, or views that record a gradient take the checked path.
+    Host logic only (CPU tensors, a stand-in engine)."""
+    import types
+    from flash_cqt.sliced import SlicedCQT
+    class Engine:                      # stand-in engine object (weakly referenced)
+        dev = torch.device("cpu")
+
+    s = SlicedCQT.__new__(SlicedCQT)
+    f = Engine()
+    s.cqt = types.SimpleNamespace(f=f)
+    s.fused_framing = True
+
+    def one_slice():
+        buf = torch.zeros(64)
+        views = SlicedCQT._stream_mark(f, [buf.as_strided((2, 4), (4, 1), 8 * i) for i in range(5)])
+        return buf, views[:3], views[3:]
+
+    buf, blocks, side = one_slice()
+    got = s._stream_buffer(blocks, side)
+    assert got is not None and got[0] is f and got[1] is buf
+    assert s._stream_buffer(blocks, [side[0], side[1].clone()]) is None          # a part replaced
+    assert s._stream_buffer(list(blocks), side[:1]) is None                      # a part missing
+    assert s._stream_buffer(blocks, None) is None
+    buf2, blocks2, side2 = one_slice()
+    assert s._stream_buffer(blocks, side2) is None                               # parts of two slices
+    assert s._stream_buffer([b.clone() for b in blocks], side) is None          # unmarked blocks
+    other = Engine()
+    s.cqt = types.SimpleNamespace(f=other)
+    assert s._stream_buffer(blocks, side) is None                                # another engine
+    s.cqt = types.SimpleNamespace(f=f)
+    s.fused_framing = False
+    assert s._stream_buffer(blocks, side) is None
+    s.fused_framing = True
+    g = torch.zeros(64, requires_grad=True)
+    gviews = SlicedCQT._stream_mark(f, [g.as_strided((2, 4), (4, 1), 8 * i) for i in range(5)])
+    assert s._stream_buffer(gviews[:3], gviews[3:]) is None                      # records a gradient
+    with torch.no_grad():
+        assert s._stream_buffer(gviews[:3], gviews[3:]) is not None
