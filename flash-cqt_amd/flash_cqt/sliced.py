@@ -217,8 +217,9 @@ class SlicedCQT:
         return f
 
     def _caches(self, f):
-        """Buffer caches of engine f; swapping self.cqt drops the old ones (the
-        slot buffer F belongs to one engine's scatter table)."""
+        """Caches of engine f (its buffer set; raw pointers and streamed view
+        arguments); swapping self.cqt drops the old ones (the slot buffer F
+        belongs to one engine's scatter table, view arguments to its layout)."""
         if self.__dict__.get("_cache_owner") is not f:
             self.__dict__.update(_cache_owner=f, _fused_ws={}, _stream_ptr_cache={})
         return self.__dict__["_fused_ws"], self.__dict__["_stream_ptr_cache"]
@@ -439,9 +440,10 @@ class SlicedCQT:
 
     def _stream_view_args(self, f, B, C):
         """as_strided arguments of one streamed slice's group views
-        [B, C, bins, M] into its coefficient buffer (cached per B, C)."""
-        cache = self.__dict__.setdefault("_stream_view_cache", {})
-        key = (id(f), B, C)
+        [B, C, bins, M] into its coefficient buffer (cached per B, C with the
+        engine's other per-engine caches, which a new engine replaces)."""
+        cache = self._caches(f)[1]
+        key = ("views", B, C)
         args = cache.get(key)
         if args is None:
             nsig = B * C

@@ -598,3 +598,22 @@ def test_stream_bwd_recognises_only_the_marked_views_cpu():
     assert s._stream_buffer(gviews[:3], gviews[3:]) is None                      # records a gradient
     with torch.no_grad():
         assert s._stream_buffer(gviews[:3], gviews[3:]) is not None
+
+
+def test_stream_view_arguments_follow_the_engine_cpu():
+    """The streamed slice's view arguments are cached with the engine's
+    other caches: another engine (another layout) gets its own, computed
+    from its own group table. Host logic only (stand-in engines)."""
+    from flash_cqt.sliced import SlicedCQT
+
+    class Engine:
+        def __init__(self, gspec):
+            self.gspec = gspec
+
+    s = SlicedCQT.__new__(SlicedCQT)
+    a, b = Engine([(2, 4, 0), (1, 8, 8)]), Engine([(4, 2, 0)])
+    va = s._stream_view_args(a, 1, 3)
+    assert va == [((1, 3, 2, 4), (24, 8, 4, 1), 0), ((1, 3, 1, 8), (24, 8, 8, 1), 24)]
+    assert s._stream_view_args(a, 1, 3) is va                       # cached
+    assert s._stream_view_args(b, 1, 3) == [((1, 3, 4, 2), (24, 8, 2, 1), 0)]
+    assert s._stream_view_args(a, 1, 3) == va and s._stream_view_args(a, 1, 3) is not va   # rebuilt for a
